@@ -1,0 +1,196 @@
+"""The tm_* C ABI end to end on the device (reference CABITests.swift:93-318,
+python/tests/test_plugin_shape.py:183-300).  The reference compiles its test
+kernels from ttir; here they are HIP source compiled for gfx950 by the
+library's hiprtc path, or a code object built by hipcc."""
+
+import array
+import ctypes
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+VECTOR_ADD = r"""
+extern "C" __global__ void add_kernel(const float *a, const float *b, float *out, int n) {
+  const int start = blockIdx.x * 1024, end = min(n, start + 1024);
+  for (int i = start + threadIdx.x; i < end; i += blockDim.x) out[i] = a[i] + b[i];
+}
+"""
+
+SCALE_BIAS = r"""
+extern "C" __global__ void scale_bias_kernel(const float *x, float *y, float scale, float bias,
+                                             int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) y[i] = x[i] * scale + bias;
+}
+"""
+
+I64_KERNEL = r"""
+extern "C" __global__ void i64_kernel(long long *out, long long base, int n) {
+  const int i = blockIdx.x * 8 + threadIdx.x;
+  if (threadIdx.x < 8 && i < n) out[i] = base + i;
+}
+"""
+
+COPY = r"""
+extern "C" __global__ void copy_kernel(const float *x, float *y) { y[threadIdx.x] = x[threadIdx.x]; }
+"""
+
+
+def _upload(core, values):
+    data = array.array("f", values)
+    handle = core.alloc_buffer(4 * len(data))
+    core.buffer_write(handle, 0, data.buffer_info()[0], 4 * len(data))
+    return handle
+
+
+def _download(core, handle, n, code="f"):
+    out = array.array(code, [0] * n)
+    core.buffer_read(handle, 0, out.buffer_info()[0], out.itemsize * n)
+    return out
+
+
+def test_probe_passed(core, device):
+    assert core.is_usable()
+    assert core.unusable_reason() is None
+    assert "gfx950" in device
+
+
+def test_vector_add_round_trips_through_the_c_abi(core, device):
+    n = 5000
+    a = [i * 0.5 for i in range(n)]
+    b = [float(i % 13) for i in range(n)]
+    live = core.live_handle_count()
+    library = core.compile_msl(VECTOR_ADD)
+    kernel = core.load_kernel(library, "add_kernel")
+    assert core.kernel_max_threads(kernel) >= 128
+    ba, bb = _upload(core, a), _upload(core, b)
+    out = core.alloc_buffer(4 * n)
+    assert core.buffer_length(out) == 4 * n
+    core.launch(kernel, ((n + 1023) // 1024, 1, 1), 128,
+                [core.ARG_BUFFER] * 3 + [core.ARG_I32], [ba, bb, out, n])
+    assert list(_download(core, out, n)) == [x + y for x, y in zip(a, b)]
+    # Reading past the end is refused rather than corrupting the host.
+    host = (ctypes.c_float * n)()
+    assert core._lib.tm_buffer_read(out, 4, host, 4 * n) == -1
+    assert "exceeds the" in core.last_error()
+    for h in (ba, bb, out):
+        core.free_buffer(h)
+    core.release_kernel(kernel)
+    core.release_library(library)
+    assert core.live_handle_count() == live
+
+
+def test_float_scalar_launch_arguments(core, device):
+    n = 64
+    library = core.compile_msl(SCALE_BIAS)
+    kernel = core.load_kernel(library, "scale_bias_kernel")
+    bin_, bout = _upload(core, [float(i) for i in range(n)]), core.alloc_buffer(4 * n)
+    try:
+        core.launch(kernel, (1, 1, 1), 128,
+                    [core.ARG_BUFFER, core.ARG_BUFFER, core.ARG_F32, core.ARG_F32, core.ARG_I32],
+                    [bin_, bout, core.float_bits(2.5), core.float_bits(-1.75), n])
+        assert list(_download(core, bout, n)) == [i * 2.5 - 1.75 for i in range(n)]
+        assert core._lib.tm_launch(kernel, 1, 1, 1, 128, None, None, 5) == -1
+        assert "NULL argument arrays" in core.last_error()
+    finally:
+        core.free_buffer(bin_)
+        core.free_buffer(bout)
+        core.release_kernel(kernel)
+        core.release_library(library)
+
+
+def test_i64_scalar_arguments_survive_the_launch_abi(core, device):
+    base, n = 1 << 40, 24
+    library = core.compile_msl(I64_KERNEL)
+    kernel = core.load_kernel(library, "i64_kernel")
+    out = core.alloc_buffer(8 * n)
+    try:
+        core.launch(kernel, (3, 1, 1), 64, [core.ARG_BUFFER, core.ARG_I64, core.ARG_I32],
+                    [out, base, n])
+        assert list(_download(core, out, n, "q")) == [base + i for i in range(n)]
+    finally:
+        core.free_buffer(out)
+        core.release_kernel(kernel)
+        core.release_library(library)
+
+
+def test_compile_errors_surface_as_zero_handle(core, device):
+    assert core._lib.tm_compile_msl(b"not hip at all") == 0
+    assert "HIP compilation failed" in core.last_error()
+
+
+def test_buffer_contents_is_the_device_address(core, device):
+    handle = core.alloc_buffer(16)
+    try:
+        assert core.buffer_contents(handle) % 256 == 0
+        value = ctypes.c_float(1.25)
+        core.buffer_write(handle, 4, ctypes.addressof(value), 4)
+        out = _download(core, handle, 2)
+        assert out[1] == 1.25
+    finally:
+        core.free_buffer(handle)
+
+
+def test_code_object_loading_through_the_abi(core, device, tmp_path):
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.fail("hipcc is missing on a GPU box")
+    src = tmp_path / "copy.hip"
+    src.write_text("#include <hip/hip_runtime.h>\n" + COPY)
+    image_path = tmp_path / "copy.hsaco"
+    subprocess.run([hipcc, "--offload-arch=gfx950", "--genco", "-O2", str(src), "-o",
+                    str(image_path)], check=True, timeout=120)
+    image = image_path.read_bytes()
+    library = core.load_metallib(image)
+    kernel = core.load_kernel(library, "copy_kernel")
+    src_buf = _upload(core, [float(i) for i in range(64)])
+    dst_buf = core.alloc_buffer(256)
+    try:
+        core.launch(kernel, (1, 1, 1), 64, [core.ARG_BUFFER] * 2, [src_buf, dst_buf])
+        assert list(_download(core, dst_buf, 64)) == [float(i) for i in range(64)]
+    finally:
+        core.free_buffer(src_buf)
+        core.free_buffer(dst_buf)
+        core.release_kernel(kernel)
+        core.release_library(library)
+    garbage = bytes([0xAB] * 64)
+    assert core._lib.tm_load_metallib(garbage, 64) == 0
+    assert "could not load metallib" in core.last_error()
+
+
+def test_device_buffer_exposes_data_ptr(core, device):
+    from triton_metal.buffer import MetalBuffer
+    live = core.live_handle_count()
+    buffer = MetalBuffer((4, 8), "float32")
+    try:
+        assert buffer.nbytes == 128
+        assert buffer.data_ptr() % 16 == 0
+        source = array.array("f", [1.5] * 32)
+        buffer.copy_from(source.buffer_info()[0])
+        assert buffer.tolist()[:3] == [1.5, 1.5, 1.5]
+        bf = MetalBuffer(8, "bfloat16")
+        assert bf.itemsize == 2 and bf.nbytes == 16
+        bf.write(np.arange(8, dtype=np.float32))
+        assert list(bf.float32()) == list(range(8))
+        bf.free()
+    finally:
+        buffer.free()
+    assert core.live_handle_count() == live
+
+
+def test_builtin_launch_checks_buffer_extents(core, device):
+    lib = core.compile_msl("builtin element=f32")
+    kernel = core.load_kernel(lib, "matmul_kernel")
+    small = core.alloc_buffer(64)
+    try:
+        with pytest.raises(RuntimeError, match="needs 4096 bytes but its buffer holds 64"):
+            core.launch(kernel, (1, 1, 1), 128, [0, 0, 0] + [1] * 9,
+                        [small, small, small, 32, 32, 32, 32, 1, 32, 1, 32, 1])
+    finally:
+        core.free_buffer(small)
+        core.release_kernel(kernel)
+        core.release_library(lib)

@@ -1,0 +1,85 @@
+/*
+ * Device helpers shared by the gfx950 kernels: element types, conversions, MFMA
+ * wrappers and wavefront reductions.  CDNA4 only: 64-lane wavefronts, MFMA
+ * matrix cores, 160 KB LDS per CU.
+ *
+ * MFMA operand layouts used throughout (lane l in [0, 64), g = l / 16):
+ *   v_mfma_f32_16x16x4_f32    A: row l%16, k = g          B: col l%16, k = g
+ *   v_mfma_f32_16x16x32_bf16  A: row l%16, k = 8g .. 8g+7 B: col l%16, k = 8g .. 8g+7
+ *   (and _f16)                D: col l%16, rows 4g .. 4g+3 (4 floats)
+ * The contraction index k may be permuted freely as long as A and B use the
+ * same permutation; the attention kernels rely on that to feed the softmax
+ * output (rows 4g..4g+3 of a 16-row tile) straight back in as a B operand.
+ */
+#ifndef TM_KERNELS_COMMON_H
+#define TM_KERNELS_COMMON_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../tm_args.h"
+
+#define TM_DEV __device__ __forceinline__
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+
+/* ---- conversions ---------------------------------------------------------- */
+
+template <typename T> TM_DEV float to_f32(T x) { return (float)x; }
+
+/* Round-to-nearest-even narrowing (clang lowers (__bf16)f and (_Float16)f to
+ * the gfx950 RNE conversions). */
+template <typename T> TM_DEV T from_f32(float x) { return (T)x; }
+template <> TM_DEV float from_f32<float>(float x) { return x; }
+
+/* The value a float takes after a round trip through T: how the reference's
+ * truncf of P and dS before the second dot is reproduced in an fp32 dot. */
+template <typename T> TM_DEV float round_through(float x) { return (float)(T)x; }
+template <> TM_DEV float round_through<float>(float x) { return x; }
+
+/* ---- MFMA ----------------------------------------------------------------- */
+
+TM_DEV f32x4 mfma_f32_16x16x4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+TM_DEV f32x4 mfma_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+TM_DEV f32x4 mfma_16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+/* ---- wavefront reductions over the four 16-lane groups --------------------- */
+
+TM_DEV float group4_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16, 64));
+  x = fmaxf(x, __shfl_xor(x, 32, 64));
+  return x;
+}
+TM_DEV float group4_sum(float x) {
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+TM_DEV float wave_sum(float x) {
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+/* log2(e), written out: the reference folds sm_scale into the exp2 domain with
+ * this constant (Sources/TritonMetalBench/AttentionKernel.swift:79-80). */
+#define TM_LOG2E 1.44269504088896340736f
+
+#endif

@@ -1,0 +1,476 @@
+/*
+ * Generic gfx950 kernels for the dense hot path: every element type the
+ * reference supports (f32, f16, bf16), arbitrary strides, ragged shapes, any
+ * head dimension up to 128, causal or not.  They stage tiles through LDS as
+ * f32 and contract on v_mfma_f32_16x16x4_f32, which multiplies exactly for all
+ * three element types, so one code path serves them all.  The hot shapes run
+ * on the specialised kernels in gemm_fast.hip / attn_fast.hip; these cover
+ * everything else with the reference's numerics:
+ *   - f32 accumulation everywhere (GEMMKernel.swift:46, AttentionKernel.swift:59-65);
+ *   - P and dS rounded to the element type before the dot they feed
+ *     (AttentionKernel.swift:59-65, AttentionBackwardKernel.swift:155-160, :357-369);
+ *   - exp2 with sm_scale folded into log2(e) (AttentionKernel.swift:79-80);
+ *   - the log2-unit row statistic L = m + log2(l) (AttentionKernel.swift:33-39).
+ */
+#include "common.h"
+
+#define TM_NEG_INF (-__builtin_inff())
+
+/* ---------------------------------------------------------------------------
+ * matmul_kernel: C = A @ B, masked in M, N and K, f32 accumulation, output in
+ * the element type (GEMMKernel.swift:28-174; matmul.py:20-44).
+ * 64x64 output tile per 256-thread workgroup, 4 waves in 2x2, 32x32 per wave.
+ * ------------------------------------------------------------------------- */
+template <typename T>
+TM_DEV void gemm_generic(const TmGemmArgs &p) {
+  constexpr int BM = 64, BN = 64, BK = 16;
+  __shared__ float As[BM][BK + 1];
+  __shared__ float Bs[BK][BN + 4];
+  const T *A = (const T *)p.a;
+  const T *B = (const T *)p.b;
+  T *C = (T *)p.c;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+
+  f32x4 acc[2][2];
+  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = 0; k0 < p.k; k0 += BK) {
+    for (int e = tid; e < BM * BK; e += 256) {
+      const int r = e / BK, kk = e % BK;
+      const int gm = m0 + r, gk = k0 + kk;
+      As[r][kk] = (gm < p.m && gk < p.k)
+                      ? to_f32(A[(int64_t)gm * p.sam + (int64_t)gk * p.sak])
+                      : 0.f;
+    }
+    for (int e = tid; e < BK * BN; e += 256) {
+      const int kk = e / BN, cc = e % BN;
+      const int gk = k0 + kk, gn = n0 + cc;
+      Bs[kk][cc] = (gk < p.k && gn < p.n)
+                       ? to_f32(B[(int64_t)gk * p.sbk + (int64_t)gn * p.sbn])
+                       : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 4) {
+      float a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[i] = As[wm * 32 + i * 16 + c][kk + g];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = Bs[kk + g][wn * 32 + j * 16 + c];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma_f32_16x16x4(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 32 + i * 16 + 4 * g + r;
+        const int col = n0 + wn * 32 + j * 16 + c;
+        if (row < p.m && col < p.n)
+          C[(int64_t)row * p.scm + (int64_t)col * p.scn] = from_f32<T>(acc[i][j][r]);
+      }
+}
+
+/* ---------------------------------------------------------------------------
+ * attn_fwd: FlashAttention-2 forward with the online softmax in the exp2
+ * domain (AttentionKernel.swift:40-250; attention_training.py:37-71).
+ * 64 queries per workgroup (16 per wave), keys in blocks of 32.
+ * Each wave computes S^T = K Q^T so that a lane owns one query (column l%16)
+ * and four keys per 16-key tile; the row statistics are then lane-local up to
+ * a reduction over the four lane groups, and O^T = V^T P^T keeps the same
+ * lane <-> query ownership for the rescale.
+ * ------------------------------------------------------------------------- */
+template <typename T, int DP, bool CAUSAL>
+TM_DEV void attn_fwd_generic(const TmAttnFwdArgs &p) {
+  constexpr int BM = 64, BN = 32, LD = DP + 1;
+  __shared__ float Ks[BN * LD];
+  __shared__ float Vs[BN * LD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int bh = blockIdx.y;
+  const int q0 = blockIdx.x * BM;
+  const int n = p.n_ctx, D = p.head_dim;
+  const int64_t base = (int64_t)bh * p.stride_head;
+  const T *Q = (const T *)p.q + base;
+  const T *K = (const T *)p.k + base;
+  const T *V = (const T *)p.v + base;
+  T *O = (T *)p.o + base;
+
+  const int qi = q0 + wave * 16 + c;
+  float q[DP / 4];
+#pragma unroll
+  for (int s = 0; s < DP / 4; ++s) {
+    const int d = 4 * s + g;
+    q[s] = (qi < n && d < D) ? to_f32(Q[(int64_t)qi * p.stride_seq + d]) : 0.f;
+  }
+  const float qk_scale = p.sm_scale * TM_LOG2E;
+  float m_i = TM_NEG_INF, l_i = 0.f;
+  f32x4 acc[DP / 16];
+#pragma unroll
+  for (int i = 0; i < DP / 16; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  const int kend = CAUSAL ? min(n, q0 + BM) : n;
+  for (int k0 = 0; k0 < kend; k0 += BN) {
+    __syncthreads();
+    for (int e = tid; e < BN * DP; e += 256) {
+      const int r = e / DP, cc = e % DP;
+      const int kj = k0 + r;
+      const bool ok = kj < n && cc < D;
+      const int64_t off = (int64_t)kj * p.stride_seq + cc;
+      Ks[r * LD + cc] = ok ? to_f32(K[off]) : 0.f;
+      Vs[r * LD + cc] = ok ? to_f32(V[off]) : 0.f;
+    }
+    __syncthreads();
+
+    float sc[2][4];
+    float mx = TM_NEG_INF;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < DP / 4; ++st)
+        s = mfma_f32_16x16x4(Ks[(t * 16 + c) * LD + 4 * st + g], q[st], s);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kj = k0 + t * 16 + 4 * g + r;
+        float v = s[r] * qk_scale;
+        if (kj >= n || (CAUSAL && kj > qi)) v = TM_NEG_INF;
+        sc[t][r] = v;
+        mx = fmaxf(mx, v);
+      }
+    }
+    mx = group4_max(mx);
+    const float m_new = fmaxf(m_i, mx);
+    float rs = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc[t][r] = exp2f(sc[t][r] - m_new);
+        rs += sc[t][r];
+      }
+    rs = group4_sum(rs);
+    const float alpha = exp2f(m_i - m_new);
+    l_i = l_i * alpha + rs;
+    m_i = m_new;
+#pragma unroll
+    for (int dt = 0; dt < DP / 16; ++dt) {
+      acc[dt] *= alpha;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[dt] = mfma_f32_16x16x4(Vs[(t * 16 + 4 * g + r) * LD + dt * 16 + c],
+                                     round_through<T>(sc[t][r]), acc[dt]);
+    }
+  }
+
+  if (qi < n) {
+    const float inv = 1.f / l_i;
+#pragma unroll
+    for (int dt = 0; dt < DP / 16; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = dt * 16 + 4 * g + r;
+        if (d < D) O[(int64_t)qi * p.stride_seq + d] = from_f32<T>(acc[dt][r] * inv);
+      }
+    if (p.lse && g == 0) p.lse[(int64_t)bh * p.stride_lse + qi] = m_i + log2f(l_i);
+  }
+}
+
+/* ---------------------------------------------------------------------------
+ * attn_bwd_preprocess: Delta_i = sum_d dO_id * O_id in f32
+ * (AttentionBackwardKernel.swift:53-136).  64 rows per workgroup.
+ * ------------------------------------------------------------------------- */
+template <typename T>
+TM_DEV void attn_pre_generic(const TmAttnPreArgs &p) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int bh = blockIdx.y;
+  const int64_t base = (int64_t)bh * p.stride_head;
+  const T *O = (const T *)p.o + base;
+  const T *dO = (const T *)p.dout + base;
+  for (int rr = 0; rr < 16; ++rr) {
+    const int row = blockIdx.x * 64 + wave * 16 + rr;
+    if (row >= p.n_ctx) break;
+    float acc = 0.f;
+    for (int d = lane; d < p.head_dim; d += 64) {
+      const int64_t off = (int64_t)row * p.stride_seq + d;
+      acc += to_f32(O[off]) * to_f32(dO[off]);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) p.delta[(int64_t)bh * p.stride_lse + row] = acc;
+  }
+}
+
+/* ---------------------------------------------------------------------------
+ * attn_bwd_dq: per key block, P = exp2(qk_scale Q K^T - L), dP = dO V^T,
+ * dS = P (dP - Delta), dQ += dS K; dQ * sm_scale on the way out
+ * (AttentionBackwardKernel.swift:151-344).  64 queries per workgroup.
+ * S^T / dP^T are formed per wave so a lane owns one query, as in attn_fwd.
+ * ------------------------------------------------------------------------- */
+template <typename T, int DP, bool CAUSAL>
+TM_DEV void attn_dq_generic(const TmAttnDqArgs &p) {
+  constexpr int BM = 64, BN = 32, LD = DP + 1;
+  __shared__ float Ks[BN * LD];
+  __shared__ float Vs[BN * LD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int bh = blockIdx.y;
+  const int q0 = blockIdx.x * BM;
+  const int n = p.n_ctx, D = p.head_dim;
+  const int64_t base = (int64_t)bh * p.stride_head;
+  const T *Q = (const T *)p.q + base;
+  const T *K = (const T *)p.k + base;
+  const T *V = (const T *)p.v + base;
+  const T *dO = (const T *)p.dout + base;
+  T *dQ = (T *)p.dq + base;
+
+  const int qi = q0 + wave * 16 + c;
+  float q[DP / 4], dov[DP / 4];
+#pragma unroll
+  for (int s = 0; s < DP / 4; ++s) {
+    const int d = 4 * s + g;
+    const bool ok = qi < n && d < D;
+    const int64_t off = (int64_t)qi * p.stride_seq + d;
+    q[s] = ok ? to_f32(Q[off]) : 0.f;
+    dov[s] = ok ? to_f32(dO[off]) : 0.f;
+  }
+  const int64_t srow = (int64_t)bh * p.stride_lse + qi;
+  const float lse = qi < n ? p.lse[srow] : 0.f;
+  const float delta = qi < n ? p.delta[srow] : 0.f;
+  const float qk_scale = p.sm_scale * TM_LOG2E;
+
+  f32x4 acc[DP / 16];
+#pragma unroll
+  for (int i = 0; i < DP / 16; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  const int kend = CAUSAL ? min(n, q0 + BM) : n;
+  for (int k0 = 0; k0 < kend; k0 += BN) {
+    __syncthreads();
+    for (int e = tid; e < BN * DP; e += 256) {
+      const int r = e / DP, cc = e % DP;
+      const int kj = k0 + r;
+      const bool ok = kj < n && cc < D;
+      const int64_t off = (int64_t)kj * p.stride_seq + cc;
+      Ks[r * LD + cc] = ok ? to_f32(K[off]) : 0.f;
+      Vs[r * LD + cc] = ok ? to_f32(V[off]) : 0.f;
+    }
+    __syncthreads();
+
+    float ds[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      f32x4 s = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < DP / 4; ++st) {
+        s = mfma_f32_16x16x4(Ks[(t * 16 + c) * LD + 4 * st + g], q[st], s);
+        dp = mfma_f32_16x16x4(Vs[(t * 16 + c) * LD + 4 * st + g], dov[st], dp);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kj = k0 + t * 16 + 4 * g + r;
+        float v = s[r] * qk_scale;
+        if (kj >= n || (CAUSAL && kj > qi)) v = TM_NEG_INF;
+        const float pr = exp2f(v - lse);
+        ds[t][r] = round_through<T>(pr * (dp[r] - delta));
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < DP / 16; ++dt)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[dt] = mfma_f32_16x16x4(Ks[(t * 16 + 4 * g + r) * LD + dt * 16 + c], ds[t][r],
+                                     acc[dt]);
+  }
+
+  if (qi < n) {
+#pragma unroll
+    for (int dt = 0; dt < DP / 16; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = dt * 16 + 4 * g + r;
+        if (d < D) dQ[(int64_t)qi * p.stride_seq + d] = from_f32<T>(acc[dt][r] * p.sm_scale);
+      }
+  }
+}
+
+/* ---------------------------------------------------------------------------
+ * attn_bwd_dkdv: per query block, P^T = exp2(qk_scale K Q^T - L),
+ * dV += P^T dO, dP^T = V dO^T, dS^T = P^T (dP^T - Delta), dK += dS^T Q;
+ * dK * sm_scale and dV on the way out (AttentionBackwardKernel.swift:354-575).
+ * 64 keys per workgroup (16 per wave); a lane owns one key.
+ * ------------------------------------------------------------------------- */
+template <typename T, int DP, bool CAUSAL>
+TM_DEV void attn_dkdv_generic(const TmAttnDkdvArgs &p) {
+  constexpr int BN = 64, BM = 32, LD = DP + 1;
+  __shared__ float Qs[BM * LD];
+  __shared__ float dOs[BM * LD];
+  __shared__ float Ls[BM];
+  __shared__ float Ds[BM];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int bh = blockIdx.y;
+  const int k0 = blockIdx.x * BN;
+  const int n = p.n_ctx, D = p.head_dim;
+  const int64_t base = (int64_t)bh * p.stride_head;
+  const T *Q = (const T *)p.q + base;
+  const T *K = (const T *)p.k + base;
+  const T *V = (const T *)p.v + base;
+  const T *dO = (const T *)p.dout + base;
+  T *dK = (T *)p.dk + base;
+  T *dV = (T *)p.dv + base;
+  const float *Lrow = p.lse + (int64_t)bh * p.stride_lse;
+  const float *Drow = p.delta + (int64_t)bh * p.stride_lse;
+
+  const int kj = k0 + wave * 16 + c;
+  float kt[DP / 4], vt[DP / 4];
+#pragma unroll
+  for (int s = 0; s < DP / 4; ++s) {
+    const int d = 4 * s + g;
+    const bool ok = kj < n && d < D;
+    const int64_t off = (int64_t)kj * p.stride_seq + d;
+    kt[s] = ok ? to_f32(K[off]) : 0.f;
+    vt[s] = ok ? to_f32(V[off]) : 0.f;
+  }
+  const float qk_scale = p.sm_scale * TM_LOG2E;
+  f32x4 dk[DP / 16], dv[DP / 16];
+#pragma unroll
+  for (int i = 0; i < DP / 16; ++i) {
+    dk[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    dv[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int qstart = CAUSAL ? (k0 / BM) * BM : 0;
+  for (int q0 = qstart; q0 < n; q0 += BM) {
+    __syncthreads();
+    for (int e = tid; e < BM * DP; e += 256) {
+      const int r = e / DP, cc = e % DP;
+      const int qi = q0 + r;
+      const bool ok = qi < n && cc < D;
+      const int64_t off = (int64_t)qi * p.stride_seq + cc;
+      Qs[r * LD + cc] = ok ? to_f32(Q[off]) : 0.f;
+      dOs[r * LD + cc] = ok ? to_f32(dO[off]) : 0.f;
+    }
+    if (tid < BM) {
+      const int qi = q0 + tid;
+      Ls[tid] = qi < n ? Lrow[qi] : 0.f;
+      Ds[tid] = qi < n ? Drow[qi] : 0.f;
+    }
+    __syncthreads();
+
+    float pt[2][4], dst[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      f32x4 s = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < DP / 4; ++st) {
+        s = mfma_f32_16x16x4(Qs[(t * 16 + c) * LD + 4 * st + g], kt[st], s);
+        dp = mfma_f32_16x16x4(dOs[(t * 16 + c) * LD + 4 * st + g], vt[st], dp);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = t * 16 + 4 * g + r;
+        const int qi = q0 + row;
+        float v = s[r] * qk_scale;
+        if (qi >= n || (CAUSAL && qi < kj)) v = TM_NEG_INF;
+        const float pr = exp2f(v - Ls[row]);
+        pt[t][r] = round_through<T>(pr);
+        dst[t][r] = round_through<T>(pr * (dp[r] - Ds[row]));
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < DP / 16; ++dt)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = (t * 16 + 4 * g + r) * LD + dt * 16 + c;
+          dv[dt] = mfma_f32_16x16x4(dOs[row], pt[t][r], dv[dt]);
+          dk[dt] = mfma_f32_16x16x4(Qs[row], dst[t][r], dk[dt]);
+        }
+  }
+
+  if (kj < n) {
+#pragma unroll
+    for (int dt = 0; dt < DP / 16; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = dt * 16 + 4 * g + r;
+        if (d < D) {
+          const int64_t off = (int64_t)kj * p.stride_seq + d;
+          dK[off] = from_f32<T>(dk[dt][r] * p.sm_scale);
+          dV[off] = from_f32<T>(dv[dt][r]);
+        }
+      }
+  }
+}
+
+/* ---------------------------------------------------------------------------
+ * tm_probe: one MFMA against the identity plus a plain store; out[i] == i for
+ * i < 256 on a working device (the reference's probe idea, Runtime.swift:125-178).
+ * ------------------------------------------------------------------------- */
+extern "C" __global__ __launch_bounds__(64) void tm_probe(float *out) {
+  const int l = threadIdx.x, g = l >> 4, c = l & 15;
+  bf16x8 a, b;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int k = 8 * g + s;
+    a[s] = (bf16_t)(c == k ? 1.f : 0.f);
+    b[s] = (bf16_t)(k < 16 ? (float)(k * 16 + c) : 0.f);
+  }
+  f32x4 d = mfma_16x16x32(a, b, (f32x4){0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+  for (int r = 0; r < 4; ++r) out[(4 * g + r) * 16 + c] = d[r];
+}
+
+/* ---- named instantiations (the symbols the runtime looks up) -------------- */
+
+#define TM_GEMM(T, NAME) \
+  extern "C" __global__ __launch_bounds__(256) void NAME(TmGemmArgs p) { gemm_generic<T>(p); }
+TM_GEMM(float, tm_gemm_generic_f32)
+TM_GEMM(f16_t, tm_gemm_generic_f16)
+TM_GEMM(bf16_t, tm_gemm_generic_bf16)
+
+#define TM_PRE(T, NAME) \
+  extern "C" __global__ __launch_bounds__(256) void NAME(TmAttnPreArgs p) { attn_pre_generic<T>(p); }
+TM_PRE(float, tm_attn_pre_generic_f32)
+TM_PRE(f16_t, tm_attn_pre_generic_f16)
+TM_PRE(bf16_t, tm_attn_pre_generic_bf16)
+
+#define TM_ATTN_ONE(T, TN, DP, CAUSAL, CN)                                                    \
+  extern "C" __global__ __launch_bounds__(256) void tm_attn_fwd_generic_##TN##_d##DP##CN(     \
+      TmAttnFwdArgs p) {                                                                      \
+    attn_fwd_generic<T, DP, CAUSAL>(p);                                                       \
+  }                                                                                           \
+  extern "C" __global__ __launch_bounds__(256) void tm_attn_dq_generic_##TN##_d##DP##CN(      \
+      TmAttnDqArgs p) {                                                                       \
+    attn_dq_generic<T, DP, CAUSAL>(p);                                                        \
+  }                                                                                           \
+  extern "C" __global__ __launch_bounds__(256) void tm_attn_dkdv_generic_##TN##_d##DP##CN(    \
+      TmAttnDkdvArgs p) {                                                                     \
+    attn_dkdv_generic<T, DP, CAUSAL>(p);                                                      \
+  }
+#define TM_ATTN_DT(T, TN, DP)        \
+  TM_ATTN_ONE(T, TN, DP, false, )    \
+  TM_ATTN_ONE(T, TN, DP, true, _causal)
+#define TM_ATTN_ALL_DP(T, TN) \
+  TM_ATTN_DT(T, TN, 32)       \
+  TM_ATTN_DT(T, TN, 64)       \
+  TM_ATTN_DT(T, TN, 96)       \
+  TM_ATTN_DT(T, TN, 128)
+TM_ATTN_ALL_DP(float, f32)
+TM_ATTN_ALL_DP(f16_t, f16)
+TM_ATTN_ALL_DP(bf16_t, bf16)

@@ -1,0 +1,1203 @@
+/*
+ * libtritonmetal.so — the tm_* C ABI over HIP, for AMD gfx950 (MI355X).
+ *
+ * The reference's Swift core (Sources/TritonMetalCore/Runtime.swift and the
+ * @_cdecl exports in Compiler.swift:172-479) turns these entry points into
+ * Metal calls.  Here they become HIP module calls:
+ *
+ *   library  = hipModule_t  (hipModuleLoadData of a gfx950 code object, of a
+ *              hiprtc build of HIP source, or of the built-in kernel images
+ *              linked into this library)
+ *   kernel   = hipFunction_t, or a built-in kernel whose launch is planned here
+ *   buffer   = hipMalloc'd HBM
+ *   launch   = hipModuleLaunchKernel on one library-owned stream
+ *
+ * Built-in kernels carry the reference's names and argument lists
+ * (matmul_kernel, attn_fwd, attn_bwd_preprocess, attn_bwd_dq, attn_bwd_dkdv).
+ * Their planner checks every argument on the host (kinds, signs, buffer
+ * extents), picks the device function for the shape and fills a by-value
+ * argument block (tm_args.h), so no malformed request reaches the GPU.
+ */
+#include "../../include/tritonmetal.h"
+
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "tm_args.h"
+
+namespace {
+
+/* ---- errors ----------------------------------------------------------------
+ * One process-wide slot under a lock; taking it clears it
+ * (reference Compiler.swift:461-479). */
+
+struct TmError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+std::mutex g_error_lock;
+std::string g_error;
+bool g_has_error = false;
+
+void store_error(const std::string &message) {
+  std::lock_guard<std::mutex> guard(g_error_lock);
+  g_error = message;
+  g_has_error = true;
+}
+
+std::string format(const char *fmt, ...) {
+  char buf[2048];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  return buf;
+}
+
+char *dup_string(const std::string &s) { return strdup(s.c_str()); }
+
+void hip_check(hipError_t status, const char *what) {
+  if (status != hipSuccess)
+    throw TmError(format("%s failed: %s (%s)", what, hipGetErrorName(status),
+                         hipGetErrorString(status)));
+}
+
+/* ---- device ----------------------------------------------------------------*/
+
+struct Device {
+  bool present = false;
+  std::string absent_reason;
+  std::string name;
+  std::string arch;
+  hipStream_t stream = nullptr;
+};
+
+Device &device() {
+  static Device dev;
+  static std::once_flag once;
+  std::call_once(once, [] {
+    int count = 0;
+    hipError_t status = hipGetDeviceCount(&count);
+    if (status != hipSuccess || count <= 0) {
+      dev.absent_reason = format("no HIP device on this machine (hipGetDeviceCount: %s)",
+                                 hipGetErrorName(status));
+      (void)hipGetLastError();
+      return;
+    }
+    hipDeviceProp_t prop;
+    if (hipSetDevice(0) != hipSuccess || hipGetDeviceProperties(&prop, 0) != hipSuccess) {
+      dev.absent_reason = "could not query HIP device 0";
+      (void)hipGetLastError();
+      return;
+    }
+    dev.name = prop.name;
+    dev.arch = prop.gcnArchName;
+    /* Default priority on purpose: every stream of this library runs at the
+     * same priority as torch's and HIP's null stream. */
+    if (hipStreamCreateWithFlags(&dev.stream, hipStreamNonBlocking) != hipSuccess) {
+      dev.absent_reason = "could not create a HIP stream on device 0";
+      (void)hipGetLastError();
+      return;
+    }
+    dev.present = true;
+  });
+  return dev;
+}
+
+Device &require_device() {
+  Device &dev = device();
+  if (!dev.present) throw TmError("no HIP device available: " + dev.absent_reason);
+  return dev;
+}
+
+/* ---- built-in code objects --------------------------------------------------
+ * The kernel images are linked into this library by blobs.S (generated at build
+ * time) as a table of [start, end) pairs. */
+
+extern "C" {
+struct TmBlob {
+  const char *start;
+  const char *end;
+};
+extern const TmBlob tm_builtin_blob_table[];
+extern const int32_t tm_builtin_blob_count;
+}
+
+struct BuiltinModules {
+  std::vector<hipModule_t> modules;
+  std::map<std::string, hipFunction_t> functions;
+  std::mutex lock;
+};
+
+BuiltinModules &builtin_modules() {
+  static BuiltinModules mods;
+  return mods;
+}
+
+hipFunction_t builtin_function(const std::string &symbol) {
+  require_device();
+  BuiltinModules &mods = builtin_modules();
+  std::lock_guard<std::mutex> guard(mods.lock);
+  if (mods.modules.empty()) {
+    for (int i = 0; i < tm_builtin_blob_count; ++i) {
+      hipModule_t mod;
+      hip_check(hipModuleLoadData(&mod, tm_builtin_blob_table[i].start),
+                "hipModuleLoadData (built-in kernels)");
+      mods.modules.push_back(mod);
+    }
+  }
+  auto it = mods.functions.find(symbol);
+  if (it != mods.functions.end()) return it->second;
+  for (hipModule_t mod : mods.modules) {
+    hipFunction_t fn;
+    if (hipModuleGetFunction(&fn, mod, symbol.c_str()) == hipSuccess) {
+      mods.functions[symbol] = fn;
+      return fn;
+    }
+    (void)hipGetLastError();
+  }
+  throw TmError("built-in device function '" + symbol + "' is missing from the kernel images");
+}
+
+/* ---- objects and the handle table (reference Runtime.swift:250-290) -------- */
+
+enum class Kind { Library, Kernel, Buffer };
+
+struct Object {
+  virtual ~Object() = default;
+  virtual Kind kind() const = 0;
+};
+
+enum class Element { F32, F16, BF16 };
+
+const char *element_name(Element e) {
+  switch (e) {
+    case Element::F32: return "f32";
+    case Element::F16: return "f16";
+    case Element::BF16: return "bf16";
+  }
+  return "?";
+}
+int element_size(Element e) { return e == Element::F32 ? 4 : 2; }
+
+struct BuiltinSpec {
+  Element element = Element::F32;
+  int head_dim = 64;
+  bool causal = false;
+
+  std::string text() const {
+    return format("builtin element=%s head_dim=%d causal=%d", element_name(element), head_dim,
+                  causal ? 1 : 0);
+  }
+};
+
+struct Library : Object {
+  Kind kind() const override { return Kind::Library; }
+  bool builtin = false;
+  BuiltinSpec spec;
+  hipModule_t module = nullptr; /* user code object (not built-in) */
+  ~Library() override {
+    if (module) (void)hipModuleUnload(module);
+  }
+};
+
+enum class Builtin { None, Matmul, AttnFwd, AttnPre, AttnDq, AttnDkdv, Probe };
+
+struct Kernel : Object {
+  Kind kind() const override { return Kind::Kernel; }
+  std::shared_ptr<Library> library; /* keeps a user module alive */
+  std::string name;
+  Builtin builtin = Builtin::None;
+  hipFunction_t function = nullptr; /* user kernels */
+  std::mutex lock;
+  std::string last_variant;
+};
+
+struct Buffer : Object {
+  Kind kind() const override { return Kind::Buffer; }
+  void *ptr = nullptr;
+  int64_t length = 0;
+  ~Buffer() override {
+    if (ptr) (void)hipFree(ptr);
+  }
+};
+
+class HandleTable {
+ public:
+  int64_t insert(std::shared_ptr<Object> obj) {
+    std::lock_guard<std::mutex> guard(lock_);
+    const int64_t handle = next_++;
+    storage_[handle] = std::move(obj);
+    return handle;
+  }
+
+  template <typename T>
+  std::shared_ptr<T> lookup(int64_t handle, Kind kind, const char *what) {
+    std::lock_guard<std::mutex> guard(lock_);
+    auto it = storage_.find(handle);
+    if (it == storage_.end())
+      throw TmError(format("%s handle %lld is not live", what, (long long)handle));
+    if (it->second->kind() != kind)
+      throw TmError(format("handle %lld is not a %s", (long long)handle, what));
+    return std::static_pointer_cast<T>(it->second);
+  }
+
+  bool remove(int64_t handle, Kind kind) {
+    std::shared_ptr<Object> doomed;
+    {
+      std::lock_guard<std::mutex> guard(lock_);
+      auto it = storage_.find(handle);
+      if (it == storage_.end() || it->second->kind() != kind) return false;
+      doomed = std::move(it->second);
+      storage_.erase(it);
+    }
+    return true; /* the object is destroyed outside the lock */
+  }
+
+  int64_t count() {
+    std::lock_guard<std::mutex> guard(lock_);
+    return (int64_t)storage_.size();
+  }
+
+ private:
+  std::mutex lock_;
+  std::unordered_map<int64_t, std::shared_ptr<Object>> storage_;
+  int64_t next_ = 1;
+};
+
+HandleTable &handles() {
+  static HandleTable table;
+  return table;
+}
+
+/* ---- built-in library specs -------------------------------------------------
+ * "builtin [element=f32|f16|bf16] [head_dim=N] [causal=0|1]": the
+ * specialisation the reference bakes into each ttir module (the element type
+ * of every pointer argument and the HEAD_DIM constexpr) plus the causal mask,
+ * which the reference does not have. */
+
+bool is_builtin_spec(const char *text) {
+  while (*text == ' ' || *text == '\n' || *text == '\t') ++text;
+  return strncmp(text, "builtin", 7) == 0 &&
+         (text[7] == 0 || text[7] == ' ' || text[7] == '\n' || text[7] == '\t');
+}
+
+BuiltinSpec parse_spec(const char *text) {
+  std::istringstream in(text);
+  std::string word;
+  in >> word; /* "builtin" */
+  BuiltinSpec spec;
+  while (in >> word) {
+    const size_t eq = word.find('=');
+    if (eq == std::string::npos)
+      throw TmError("built-in library spec: expected key=value, got '" + word + "'");
+    const std::string key = word.substr(0, eq), value = word.substr(eq + 1);
+    if (key == "element") {
+      if (value == "f32" || value == "float32") spec.element = Element::F32;
+      else if (value == "f16" || value == "float16") spec.element = Element::F16;
+      else if (value == "bf16" || value == "bfloat16") spec.element = Element::BF16;
+      else throw TmError("built-in library spec: unsupported element '" + value + "'");
+    } else if (key == "head_dim") {
+      char *end = nullptr;
+      const long d = strtol(value.c_str(), &end, 10);
+      if (!end || *end || d < 1 || d > 128)
+        throw TmError("built-in library spec: head_dim must be an integer in 1..128, got '" +
+                      value + "'");
+      spec.head_dim = (int)d;
+    } else if (key == "causal") {
+      if (value == "0" || value == "false") spec.causal = false;
+      else if (value == "1" || value == "true") spec.causal = true;
+      else throw TmError("built-in library spec: causal must be 0 or 1, got '" + value + "'");
+    } else {
+      throw TmError("built-in library spec: unknown key '" + key + "'");
+    }
+  }
+  return spec;
+}
+
+struct BuiltinInfo {
+  Builtin id;
+  const char *name;
+  std::vector<int> kinds;  /* the reference's argument kinds, in order */
+  std::vector<const char *> dtypes;
+  int optional_tail;       /* trailing arguments that may be omitted */
+};
+
+const std::vector<BuiltinInfo> &builtin_table() {
+  static const std::vector<BuiltinInfo> table = {
+      {Builtin::Matmul, "matmul_kernel", {0, 0, 0, 1, 1, 1, 1, 1, 1, 1, 1, 1},
+       {"E", "E", "E", "i32", "i32", "i32", "i32", "i32", "i32", "i32", "i32", "i32"}, 0},
+      {Builtin::AttnFwd, "attn_fwd", {0, 0, 0, 0, 2, 1, 1, 1, 0, 1},
+       {"E", "E", "E", "E", "f32", "i32", "i32", "i32", "f32", "i32"}, 2},
+      {Builtin::AttnPre, "attn_bwd_preprocess", {0, 0, 0, 1, 1, 1, 1},
+       {"E", "E", "f32", "i32", "i32", "i32", "i32"}, 0},
+      {Builtin::AttnDq, "attn_bwd_dq", {0, 0, 0, 0, 0, 0, 0, 2, 1, 1, 1, 1},
+       {"E", "E", "E", "E", "E", "f32", "f32", "f32", "i32", "i32", "i32", "i32"}, 0},
+      {Builtin::AttnDkdv, "attn_bwd_dkdv", {0, 0, 0, 0, 0, 0, 0, 0, 2, 1, 1, 1, 1},
+       {"E", "E", "E", "E", "E", "E", "f32", "f32", "f32", "i32", "i32", "i32", "i32"}, 0},
+      {Builtin::Probe, "tm_probe", {0}, {"f32"}, 0},
+  };
+  return table;
+}
+
+const BuiltinInfo *find_builtin(const std::string &name) {
+  for (const BuiltinInfo &info : builtin_table())
+    if (name == info.name) return &info;
+  return nullptr;
+}
+
+std::string builtin_names() {
+  std::string out;
+  for (const BuiltinInfo &info : builtin_table()) {
+    if (!out.empty()) out += ", ";
+    out += info.name;
+  }
+  return out;
+}
+
+/* Workgroup shape each built-in runs at (published through tm_kernel_info). */
+struct Published {
+  int threads;
+  std::vector<int> block_shape;
+};
+
+Published published_shape(Builtin id) {
+  switch (id) {
+    case Builtin::Matmul: return {256, {64, 64}};
+    case Builtin::AttnFwd: return {256, {64}};
+    case Builtin::AttnPre: return {256, {64}};
+    case Builtin::AttnDq: return {256, {64}};
+    case Builtin::AttnDkdv: return {256, {64}};
+    case Builtin::Probe: return {64, {256}};
+    default: return {256, {1}};
+  }
+}
+
+/* ---- launch arguments ------------------------------------------------------ */
+
+struct Arg {
+  int kind;
+  int64_t value;
+  std::shared_ptr<Buffer> buffer; /* kind 0 */
+};
+
+std::vector<Arg> decode_args(const int32_t *kinds, const int64_t *values, int32_t argc) {
+  std::vector<Arg> args;
+  if (argc < 0) throw TmError(format("tm_launch received a negative argument count %d", argc));
+  if (argc > 0 && (!kinds || !values)) throw TmError("tm_launch received NULL argument arrays");
+  for (int i = 0; i < argc; ++i) {
+    Arg a{kinds[i], values[i], nullptr};
+    switch (kinds[i]) {
+      case TM_ARG_BUFFER:
+        a.buffer = handles().lookup<Buffer>(values[i], Kind::Buffer, "buffer");
+        break;
+      case TM_ARG_I32:
+      case TM_ARG_F32:
+      case TM_ARG_I64:
+        break;
+      default:
+        throw TmError(format("unknown launch argument kind %d at position %d", kinds[i], i));
+    }
+    args.push_back(a);
+  }
+  return args;
+}
+
+int32_t as_i32(const Arg &a) { return (int32_t)(uint32_t)(a.value & 0xffffffffu); }
+float as_f32(const Arg &a) {
+  const uint32_t bits = (uint32_t)(a.value & 0xffffffffu);
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+/* A planned dispatch: device function, geometry and the by-value argument block. */
+struct Plan {
+  hipFunction_t function = nullptr;
+  std::string variant;
+  unsigned grid[3] = {1, 1, 1};
+  unsigned block = 1;
+  std::vector<unsigned char> kernarg; /* packed bytes */
+  bool empty = false;                 /* nothing to compute (a zero-sized problem) */
+  bool by_value_struct = true;        /* built-in: one struct argument */
+};
+
+template <typename S>
+void set_kernarg(Plan &plan, const S &s) {
+  plan.kernarg.resize(sizeof(S));
+  memcpy(plan.kernarg.data(), &s, sizeof(S));
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+/* Elements a strided 2-D access touches, from element 0: the host-side proof
+ * that a kernel stays inside its buffer. */
+int64_t extent(int64_t rows, int64_t row_stride, int64_t cols, int64_t col_stride) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return (rows - 1) * row_stride + (cols - 1) * col_stride + 1;
+}
+
+void require_extent(const Arg &a, int64_t elements, int esize, const char *kernel, int index,
+                    const char *what) {
+  const int64_t need = elements * esize;
+  if (need > a.buffer->length)
+    throw TmError(format("%s argument %d (%s) needs %lld bytes but its buffer holds %lld", kernel,
+                         index, what, (long long)need, (long long)a.buffer->length));
+}
+
+void require_nonneg(int64_t v, const char *kernel, const char *what) {
+  if (v < 0) throw TmError(format("%s: %s must be non-negative, got %lld", kernel, what,
+                                  (long long)v));
+}
+
+void check_signature(const BuiltinInfo &info, const std::vector<Arg> &args) {
+  const int full = (int)info.kinds.size();
+  const int argc = (int)args.size();
+  if (argc != full && !(info.optional_tail && argc == full - info.optional_tail)) {
+    if (info.optional_tail)
+      throw TmError(format("%s expects %d or %d arguments, got %d", info.name,
+                           full - info.optional_tail, full, argc));
+    throw TmError(format("%s expects %d arguments, got %d", info.name, full, argc));
+  }
+  static const char *kind_names[] = {"a buffer", "an i32", "an f32", "an i64"};
+  for (int i = 0; i < argc; ++i)
+    if (args[i].kind != info.kinds[i])
+      throw TmError(format("%s argument %d must be %s (kind %d), got kind %d", info.name, i,
+                           kind_names[info.kinds[i]], info.kinds[i], args[i].kind));
+}
+
+int padded_head_dim(int d) { return d <= 32 ? 32 : d <= 64 ? 64 : d <= 96 ? 96 : 128; }
+
+std::string attn_symbol(const char *op, const BuiltinSpec &spec) {
+  return format("tm_attn_%s_generic_%s_d%d%s", op, element_name(spec.element),
+                padded_head_dim(spec.head_dim), spec.causal ? "_causal" : "");
+}
+
+void validate_attn_common(const char *name, int64_t heads, int32_t stride_head,
+                          int32_t stride_seq, int32_t n_ctx, int head_dim) {
+  require_nonneg(stride_head, name, "stride_head");
+  require_nonneg(n_ctx, name, "n_ctx");
+  if (stride_seq < head_dim && n_ctx > 1)
+    throw TmError(format("%s: stride_seq %d is smaller than head_dim %d (rows would overlap)",
+                         name, stride_seq, head_dim));
+  if (heads > 65535) throw TmError(format("%s: %lld heads exceeds 65535", name, (long long)heads));
+}
+
+Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, int64_t gx,
+                  int64_t gy, int64_t gz) {
+  const BuiltinInfo &info = *find_builtin(k.name);
+  check_signature(info, args);
+  const BuiltinSpec &spec = lib.spec;
+  const int es = element_size(spec.element);
+  const char *el = element_name(spec.element);
+  const int64_t heads = gy * gz;
+  Plan plan;
+
+  switch (info.id) {
+    case Builtin::Matmul: {
+      TmGemmArgs p{};
+      p.a = args[0].buffer->ptr;
+      p.b = args[1].buffer->ptr;
+      p.c = args[2].buffer->ptr;
+      p.m = as_i32(args[3]);
+      p.n = as_i32(args[4]);
+      p.k = as_i32(args[5]);
+      p.sam = as_i32(args[6]);
+      p.sak = as_i32(args[7]);
+      p.sbk = as_i32(args[8]);
+      p.sbn = as_i32(args[9]);
+      p.scm = as_i32(args[10]);
+      p.scn = as_i32(args[11]);
+      const char *nm = info.name;
+      require_nonneg(p.m, nm, "M");
+      require_nonneg(p.n, nm, "N");
+      require_nonneg(p.k, nm, "K");
+      require_nonneg(p.sam, nm, "stride_am");
+      require_nonneg(p.sak, nm, "stride_ak");
+      require_nonneg(p.sbk, nm, "stride_bk");
+      require_nonneg(p.sbn, nm, "stride_bn");
+      require_nonneg(p.scm, nm, "stride_cm");
+      require_nonneg(p.scn, nm, "stride_cn");
+      require_extent(args[0], extent(p.m, p.sam, p.k, p.sak), es, nm, 0, "A");
+      require_extent(args[1], extent(p.k, p.sbk, p.n, p.sbn), es, nm, 1, "B");
+      require_extent(args[2], extent(p.m, p.scm, p.n, p.scn), es, nm, 2, "C");
+      if (p.m == 0 || p.n == 0) {
+        plan.empty = true;
+        return plan;
+      }
+      plan.variant = format("tm_gemm_generic_%s", el);
+      plan.grid[0] = (unsigned)cdiv(p.m, 64);
+      plan.grid[1] = (unsigned)cdiv(p.n, 64);
+      plan.block = 256;
+      set_kernarg(plan, p);
+      break;
+    }
+    case Builtin::AttnFwd: {
+      TmAttnFwdArgs p{};
+      p.q = args[0].buffer->ptr;
+      p.k = args[1].buffer->ptr;
+      p.v = args[2].buffer->ptr;
+      p.o = args[3].buffer->ptr;
+      p.sm_scale = as_f32(args[4]);
+      p.stride_head = as_i32(args[5]);
+      p.stride_seq = as_i32(args[6]);
+      p.n_ctx = as_i32(args[7]);
+      p.head_dim = spec.head_dim;
+      p.heads = (int32_t)heads;
+      const char *nm = info.name;
+      validate_attn_common(nm, heads, p.stride_head, p.stride_seq, p.n_ctx, spec.head_dim);
+      const int64_t ext = heads > 0 && p.n_ctx > 0
+                              ? (heads - 1) * (int64_t)p.stride_head +
+                                    extent(p.n_ctx, p.stride_seq, spec.head_dim, 1)
+                              : 0;
+      for (int i = 0; i < 4; ++i) require_extent(args[i], ext, es, nm, i, "Q/K/V/O");
+      if (args.size() == 10) {
+        p.lse = (float *)args[8].buffer->ptr;
+        p.stride_lse = as_i32(args[9]);
+        require_nonneg(p.stride_lse, nm, "stride_lse");
+        require_extent(args[8], heads > 0 && p.n_ctx > 0
+                                    ? (heads - 1) * (int64_t)p.stride_lse + p.n_ctx
+                                    : 0,
+                       4, nm, 8, "L");
+      }
+      if (p.n_ctx == 0) {
+        plan.empty = true;
+        return plan;
+      }
+      plan.variant = attn_symbol("fwd", spec);
+      plan.grid[0] = (unsigned)cdiv(p.n_ctx, 64);
+      plan.grid[1] = (unsigned)heads;
+      plan.block = 256;
+      set_kernarg(plan, p);
+      break;
+    }
+    case Builtin::AttnPre: {
+      TmAttnPreArgs p{};
+      p.o = args[0].buffer->ptr;
+      p.dout = args[1].buffer->ptr;
+      p.delta = (float *)args[2].buffer->ptr;
+      p.stride_head = as_i32(args[3]);
+      p.stride_seq = as_i32(args[4]);
+      p.stride_lse = as_i32(args[5]);
+      p.n_ctx = as_i32(args[6]);
+      p.head_dim = spec.head_dim;
+      p.heads = (int32_t)heads;
+      const char *nm = info.name;
+      validate_attn_common(nm, heads, p.stride_head, p.stride_seq, p.n_ctx, spec.head_dim);
+      require_nonneg(p.stride_lse, nm, "stride_lse");
+      const int64_t ext = heads > 0 && p.n_ctx > 0
+                              ? (heads - 1) * (int64_t)p.stride_head +
+                                    extent(p.n_ctx, p.stride_seq, spec.head_dim, 1)
+                              : 0;
+      require_extent(args[0], ext, es, nm, 0, "O");
+      require_extent(args[1], ext, es, nm, 1, "dO");
+      require_extent(args[2],
+                     heads > 0 && p.n_ctx > 0 ? (heads - 1) * (int64_t)p.stride_lse + p.n_ctx : 0,
+                     4, nm, 2, "Delta");
+      if (p.n_ctx == 0) {
+        plan.empty = true;
+        return plan;
+      }
+      plan.variant = format("tm_attn_pre_generic_%s", el);
+      plan.grid[0] = (unsigned)cdiv(p.n_ctx, 64);
+      plan.grid[1] = (unsigned)heads;
+      plan.block = 256;
+      set_kernarg(plan, p);
+      break;
+    }
+    case Builtin::AttnDq:
+    case Builtin::AttnDkdv: {
+      const bool dq = info.id == Builtin::AttnDq;
+      const int first_stat = dq ? 5 : 6;
+      const float sm_scale = as_f32(args[first_stat + 2]);
+      const int32_t stride_head = as_i32(args[first_stat + 3]);
+      const int32_t stride_seq = as_i32(args[first_stat + 4]);
+      const int32_t stride_lse = as_i32(args[first_stat + 5]);
+      const int32_t n_ctx = as_i32(args[first_stat + 6]);
+      const char *nm = info.name;
+      validate_attn_common(nm, heads, stride_head, stride_seq, n_ctx, spec.head_dim);
+      require_nonneg(stride_lse, nm, "stride_lse");
+      const int64_t ext = heads > 0 && n_ctx > 0
+                              ? (heads - 1) * (int64_t)stride_head +
+                                    extent(n_ctx, stride_seq, spec.head_dim, 1)
+                              : 0;
+      for (int i = 0; i < first_stat; ++i) require_extent(args[i], ext, es, nm, i, "tensor");
+      const int64_t sext =
+          heads > 0 && n_ctx > 0 ? (heads - 1) * (int64_t)stride_lse + n_ctx : 0;
+      require_extent(args[first_stat], sext, 4, nm, first_stat, "L");
+      require_extent(args[first_stat + 1], sext, 4, nm, first_stat + 1, "Delta");
+      if (n_ctx == 0) {
+        plan.empty = true;
+        return plan;
+      }
+      plan.grid[0] = (unsigned)cdiv(n_ctx, 64);
+      plan.grid[1] = (unsigned)heads;
+      plan.block = 256;
+      if (dq) {
+        TmAttnDqArgs p{};
+        p.q = args[0].buffer->ptr;
+        p.k = args[1].buffer->ptr;
+        p.v = args[2].buffer->ptr;
+        p.dout = args[3].buffer->ptr;
+        p.dq = args[4].buffer->ptr;
+        p.lse = (const float *)args[5].buffer->ptr;
+        p.delta = (const float *)args[6].buffer->ptr;
+        p.sm_scale = sm_scale;
+        p.stride_head = stride_head;
+        p.stride_seq = stride_seq;
+        p.stride_lse = stride_lse;
+        p.n_ctx = n_ctx;
+        p.head_dim = spec.head_dim;
+        p.heads = (int32_t)heads;
+        plan.variant = attn_symbol("dq", spec);
+        set_kernarg(plan, p);
+      } else {
+        TmAttnDkdvArgs p{};
+        p.q = args[0].buffer->ptr;
+        p.k = args[1].buffer->ptr;
+        p.v = args[2].buffer->ptr;
+        p.dout = args[3].buffer->ptr;
+        p.dk = args[4].buffer->ptr;
+        p.dv = args[5].buffer->ptr;
+        p.lse = (const float *)args[6].buffer->ptr;
+        p.delta = (const float *)args[7].buffer->ptr;
+        p.sm_scale = sm_scale;
+        p.stride_head = stride_head;
+        p.stride_seq = stride_seq;
+        p.stride_lse = stride_lse;
+        p.n_ctx = n_ctx;
+        p.head_dim = spec.head_dim;
+        p.heads = (int32_t)heads;
+        plan.variant = attn_symbol("dkdv", spec);
+        set_kernarg(plan, p);
+      }
+      break;
+    }
+    case Builtin::Probe: {
+      require_extent(args[0], 256, 4, info.name, 0, "out");
+      void *out = args[0].buffer->ptr;
+      plan.variant = "tm_probe";
+      plan.block = 64;
+      set_kernarg(plan, out);
+      break;
+    }
+    default:
+      throw TmError("unknown built-in kernel");
+  }
+  (void)gx;
+  plan.function = builtin_function(plan.variant);
+  return plan;
+}
+
+/* User kernels: pack the arguments with natural alignment (pointers and i64 on
+ * 8 bytes, i32 and f32 on 4) — the AMDGPU kernarg layout of a kernel whose
+ * parameters are declared in the same order. */
+Plan plan_user(Kernel &k, const std::vector<Arg> &args, int64_t gx, int64_t gy, int64_t gz,
+               int64_t threads) {
+  Plan plan;
+  plan.function = k.function;
+  plan.variant = k.name;
+  plan.by_value_struct = false;
+  plan.grid[0] = (unsigned)gx;
+  plan.grid[1] = (unsigned)gy;
+  plan.grid[2] = (unsigned)gz;
+  plan.block = (unsigned)threads;
+  auto &buf = plan.kernarg;
+  auto put = [&buf](const void *src, size_t size) {
+    while (buf.size() % size) buf.push_back(0);
+    const size_t at = buf.size();
+    buf.resize(at + size);
+    memcpy(buf.data() + at, src, size);
+  };
+  for (const Arg &a : args) {
+    switch (a.kind) {
+      case TM_ARG_BUFFER: {
+        void *p = a.buffer->ptr;
+        put(&p, 8);
+        break;
+      }
+      case TM_ARG_I32: {
+        int32_t v = as_i32(a);
+        put(&v, 4);
+        break;
+      }
+      case TM_ARG_F32: {
+        float f = as_f32(a);
+        put(&f, 4);
+        break;
+      }
+      case TM_ARG_I64: {
+        int64_t v = a.value;
+        put(&v, 8);
+        break;
+      }
+    }
+  }
+  while (buf.size() % 8) buf.push_back(0);
+  return plan;
+}
+
+int64_t max_threads(Kernel &k) {
+  if (k.builtin != Builtin::None) return k.builtin == Builtin::Probe ? 64 : 1024;
+  int value = 0;
+  hip_check(hipFuncGetAttribute(&value, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, k.function),
+            "hipFuncGetAttribute");
+  return value;
+}
+
+void enqueue(const Plan &plan, hipStream_t stream) {
+  if (plan.empty) return;
+  if (plan.by_value_struct) {
+    void *params[] = {(void *)plan.kernarg.data()};
+    hip_check(hipModuleLaunchKernel(plan.function, plan.grid[0], plan.grid[1], plan.grid[2],
+                                    plan.block, 1, 1, 0, stream, params, nullptr),
+              "hipModuleLaunchKernel");
+  } else {
+    size_t size = plan.kernarg.size();
+    void *data = size ? (void *)plan.kernarg.data() : nullptr;
+    void *extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, data, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
+                     HIP_LAUNCH_PARAM_END};
+    hip_check(hipModuleLaunchKernel(plan.function, plan.grid[0], plan.grid[1], plan.grid[2],
+                                    plan.block, 1, 1, 0, stream, nullptr, size ? extra : nullptr),
+              "hipModuleLaunchKernel");
+  }
+}
+
+/* Validation shared by every launch form (reference Runtime.swift:201-211),
+ * then the plan.  No HIP call happens before the request is known to be good
+ * except the device lookup the built-in planner needs. */
+Plan prepare(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads,
+             const int32_t *kinds, const int64_t *values, int32_t argc,
+             std::shared_ptr<Kernel> &k_out) {
+  auto k = handles().lookup<Kernel>(kernel, Kind::Kernel, "kernel");
+  k_out = k;
+  std::vector<Arg> args = decode_args(kinds, values, argc);
+  if (gx <= 0 || gy <= 0 || gz <= 0)
+    throw TmError("threadgroup grid must be positive in every dimension");
+  if (gx > 0x7fffffff || gy > 0xffff || gz > 0xffff)
+    throw TmError("threadgroup grid exceeds the device's grid limits");
+  if (threads <= 0) throw TmError("threadsPerThreadgroup must be positive");
+  const int64_t limit = k->builtin != Builtin::None ? max_threads(*k) : -1;
+  if (limit > 0 && threads > limit)
+    throw TmError(format("threadsPerThreadgroup %lld exceeds the pipeline maximum %lld",
+                         (long long)threads, (long long)limit));
+  Plan plan;
+  if (k->builtin != Builtin::None) {
+    plan = plan_builtin(*k, *k->library, args, gx, gy, gz);
+  } else {
+    require_device();
+    const int64_t user_limit = max_threads(*k);
+    if (threads > user_limit)
+      throw TmError(format("threadsPerThreadgroup %lld exceeds the pipeline maximum %lld",
+                           (long long)threads, (long long)user_limit));
+    plan = plan_user(*k, args, gx, gy, gz, threads);
+  }
+  {
+    std::lock_guard<std::mutex> guard(k->lock);
+    k->last_variant = plan.empty ? std::string("(empty)") : plan.variant;
+  }
+  return plan;
+}
+
+void finish(hipStream_t stream) {
+  hipError_t status = hipStreamSynchronize(stream);
+  if (status != hipSuccess)
+    throw TmError(format("kernel execution failed: %s (%s)", hipGetErrorName(status),
+                         hipGetErrorString(status)));
+}
+
+/* ---- the probe (reference Runtime.swift:112-178) --------------------------- */
+
+std::string probe_device() {
+  Device &dev = device();
+  if (!dev.present) return dev.absent_reason;
+  if (dev.arch.rfind("gfx950", 0) != 0)
+    return format("%s is %s; this library's kernels are built for gfx950", dev.name.c_str(),
+                  dev.arch.c_str());
+  try {
+    hipFunction_t fn = builtin_function("tm_probe");
+    float *out = nullptr;
+    hip_check(hipMalloc(&out, 256 * sizeof(float)), "hipMalloc");
+    std::unique_ptr<float, void (*)(float *)> guard(out, [](float *p) { (void)hipFree(p); });
+    hip_check(hipMemsetAsync(out, 0, 256 * sizeof(float), dev.stream), "hipMemsetAsync");
+    void *params[] = {&out};
+    hip_check(hipModuleLaunchKernel(fn, 1, 1, 1, 64, 1, 1, 0, dev.stream, params, nullptr),
+              "hipModuleLaunchKernel");
+    finish(dev.stream);
+    float host[256];
+    hip_check(hipMemcpy(host, out, sizeof host, hipMemcpyDeviceToHost), "hipMemcpy");
+    for (int i = 0; i < 256; ++i)
+      if (host[i] != (float)i)
+        return format("%s ran the probe kernel but returned %g at %d instead of %d — its MFMA "
+                      "support is not usable",
+                      dev.name.c_str(), host[i], i, i);
+    return "";
+  } catch (const std::exception &e) {
+    return format("%s cannot run a built-in kernel: %s", dev.name.c_str(), e.what());
+  }
+}
+
+const std::string &unusable_reason() {
+  static std::string reason;
+  static std::once_flag once;
+  std::call_once(once, [] { reason = probe_device(); });
+  return reason;
+}
+
+/* ---- hiprtc ------------------------------------------------------------------ */
+
+std::vector<char> compile_hip_source(const char *source) {
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, source, "tm_user.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+    throw TmError("HIP compilation failed: hiprtcCreateProgram");
+  const char *options[] = {"--offload-arch=gfx950", "-O3"};
+  hiprtcResult status = hiprtcCompileProgram(prog, 2, options);
+  if (status != HIPRTC_SUCCESS) {
+    size_t log_size = 0;
+    hiprtcGetProgramLogSize(prog, &log_size);
+    std::string log(log_size, '\0');
+    if (log_size) hiprtcGetProgramLog(prog, &log[0]);
+    hiprtcDestroyProgram(&prog);
+    throw TmError("HIP compilation failed: " + log);
+  }
+  size_t code_size = 0;
+  hiprtcGetCodeSize(prog, &code_size);
+  std::vector<char> code(code_size);
+  hiprtcGetCode(prog, code.data());
+  hiprtcDestroyProgram(&prog);
+  return code;
+}
+
+int64_t launch_common(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads,
+                      const int32_t *kinds, const int64_t *values, int32_t argc, bool wait,
+                      int32_t repeats, float *elapsed_ms) {
+  std::shared_ptr<Kernel> k;
+  Plan plan = prepare(kernel, gx, gy, gz, threads, kinds, values, argc, k);
+  Device &dev = require_device();
+  if (repeats <= 0) {
+    enqueue(plan, dev.stream);
+    if (wait) finish(dev.stream);
+    return 0;
+  }
+  hipEvent_t start, stop;
+  hip_check(hipEventCreate(&start), "hipEventCreate");
+  hip_check(hipEventCreate(&stop), "hipEventCreate");
+  std::unique_ptr<void, std::function<void(void *)>> guard((void *)1, [&](void *) {
+    (void)hipEventDestroy(start);
+    (void)hipEventDestroy(stop);
+  });
+  hip_check(hipEventRecord(start, dev.stream), "hipEventRecord");
+  for (int i = 0; i < repeats; ++i) enqueue(plan, dev.stream);
+  hip_check(hipEventRecord(stop, dev.stream), "hipEventRecord");
+  finish(dev.stream);
+  float ms = 0.f;
+  hip_check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
+  if (elapsed_ms) *elapsed_ms = ms;
+  return 0;
+}
+
+std::string kernel_info_json(const BuiltinSpec &spec) {
+  std::ostringstream out;
+  out << "{\n  \"kernels\" : [\n";
+  bool first = true;
+  for (const BuiltinInfo &info : builtin_table()) {
+    const Published pub = published_shape(info.id);
+    if (!first) out << ",\n";
+    first = false;
+    out << "    {\n      \"args\" : [";
+    for (size_t i = 0; i < info.kinds.size(); ++i) {
+      const char *dt = strcmp(info.dtypes[i], "E") == 0 ? element_name(spec.element)
+                                                         : info.dtypes[i];
+      out << (i ? ", " : "") << "{\"dtype\" : \"" << dt << "\", \"index\" : " << i
+          << ", \"kind\" : " << info.kinds[i] << "}";
+    }
+    out << "],\n      \"block_shape\" : [";
+    for (size_t i = 0; i < pub.block_shape.size(); ++i)
+      out << (i ? ", " : "") << pub.block_shape[i];
+    out << "],\n      \"block_size\" : " << pub.block_shape[0] << ",\n      \"causal\" : "
+        << (spec.causal ? "true" : "false") << ",\n      \"head_dim\" : " << spec.head_dim
+        << ",\n      \"name\" : \"" << info.name << "\",\n      \"threads_per_threadgroup\" : "
+        << pub.threads << "\n    }";
+  }
+  out << "\n  ]\n}";
+  return out.str();
+}
+
+}  // namespace
+
+/* =============================================================================
+ * The C ABI.
+ * ===========================================================================*/
+
+#define TM_GUARD_BEGIN try {
+#define TM_GUARD_END(sentinel)              \
+  }                                         \
+  catch (const std::exception &e) {         \
+    store_error(e.what());                  \
+    return sentinel;                        \
+  }
+
+extern "C" {
+
+char *tm_version(void) { return dup_string("0.0.1"); }
+
+void tm_free(void *ptr) { free(ptr); }
+
+char *tm_last_error(void) {
+  std::lock_guard<std::mutex> guard(g_error_lock);
+  std::string message = g_has_error ? g_error : std::string("no error");
+  g_has_error = false;
+  g_error.clear();
+  return dup_string(message);
+}
+
+int32_t tm_is_active(void) { return device().present ? 1 : 0; }
+
+int32_t tm_is_usable(void) { return unusable_reason().empty() ? 1 : 0; }
+
+char *tm_unusable_reason(void) {
+  const std::string &reason = unusable_reason();
+  return reason.empty() ? nullptr : dup_string(reason);
+}
+
+char *tm_device_name(void) {
+  Device &dev = device();
+  if (!dev.present) return nullptr;
+  return dup_string(dev.name + " (" + dev.arch + ")");
+}
+
+char *tm_emit_msl(const char *module, int32_t num_simdgroups) {
+  (void)num_simdgroups;
+  TM_GUARD_BEGIN
+  if (!module) throw TmError("tm_emit_msl received a NULL module");
+  if (!is_builtin_spec(module))
+    throw TmError("tm_emit_msl: ttir lowering is not part of this library; pass a built-in "
+                  "library spec (\"builtin element=... head_dim=... causal=...\")");
+  return dup_string(parse_spec(module).text());
+  TM_GUARD_END(nullptr)
+}
+
+char *tm_kernel_info(const char *module, int32_t num_simdgroups) {
+  (void)num_simdgroups;
+  TM_GUARD_BEGIN
+  if (!module) throw TmError("tm_kernel_info received a NULL module");
+  if (!is_builtin_spec(module))
+    throw TmError("tm_kernel_info: ttir lowering is not part of this library; pass a built-in "
+                  "library spec (\"builtin element=... head_dim=... causal=...\")");
+  return dup_string(kernel_info_json(parse_spec(module)));
+  TM_GUARD_END(nullptr)
+}
+
+int64_t tm_compile_msl(const char *source) {
+  TM_GUARD_BEGIN
+  if (!source) throw TmError("tm_compile_msl received NULL source");
+  auto lib = std::make_shared<Library>();
+  if (is_builtin_spec(source)) {
+    lib->builtin = true;
+    lib->spec = parse_spec(source);
+  } else {
+    std::vector<char> code = compile_hip_source(source);
+    require_device();
+    hip_check(hipModuleLoadData(&lib->module, code.data()), "could not load compiled HIP code");
+  }
+  return handles().insert(lib);
+  TM_GUARD_END(0)
+}
+
+int64_t tm_load_metallib(const void *image, int64_t length) {
+  TM_GUARD_BEGIN
+  if (!image || length <= 0) throw TmError("tm_load_metallib received an empty image");
+  require_device();
+  std::vector<char> copy((const char *)image, (const char *)image + length);
+  auto lib = std::make_shared<Library>();
+  hipError_t status = hipModuleLoadData(&lib->module, copy.data());
+  if (status != hipSuccess) {
+    lib->module = nullptr;
+    (void)hipGetLastError();
+    throw TmError(format("could not load metallib: the image is not a loadable gfx950 code "
+                         "object (%s)",
+                         hipGetErrorName(status)));
+  }
+  return handles().insert(lib);
+  TM_GUARD_END(0)
+}
+
+int32_t tm_release_library(int64_t library) {
+  TM_GUARD_BEGIN
+  if (!handles().remove(library, Kind::Library))
+    throw TmError(format("library handle %lld is not live", (long long)library));
+  return 0;
+  TM_GUARD_END(-1)
+}
+
+int64_t tm_load_kernel(int64_t library, const char *name) {
+  TM_GUARD_BEGIN
+  if (!name) throw TmError("tm_load_kernel received a NULL kernel name");
+  auto lib = handles().lookup<Library>(library, Kind::Library, "library");
+  auto k = std::make_shared<Kernel>();
+  k->library = lib;
+  k->name = name;
+  if (lib->builtin) {
+    const BuiltinInfo *info = find_builtin(name);
+    if (!info)
+      throw TmError(format("kernel '%s' not found in library (available: %s)", name,
+                           builtin_names().c_str()));
+    k->builtin = info->id;
+  } else {
+    hipError_t status = hipModuleGetFunction(&k->function, lib->module, name);
+    if (status != hipSuccess) {
+      (void)hipGetLastError();
+      throw TmError(format("kernel '%s' not found in library (%s)", name,
+                           hipGetErrorName(status)));
+    }
+  }
+  return handles().insert(k);
+  TM_GUARD_END(0)
+}
+
+int64_t tm_kernel_max_threads(int64_t kernel) {
+  TM_GUARD_BEGIN
+  auto k = handles().lookup<Kernel>(kernel, Kind::Kernel, "kernel");
+  return max_threads(*k);
+  TM_GUARD_END(-1)
+}
+
+int32_t tm_release_kernel(int64_t kernel) {
+  TM_GUARD_BEGIN
+  if (!handles().remove(kernel, Kind::Kernel))
+    throw TmError(format("kernel handle %lld is not live", (long long)kernel));
+  return 0;
+  TM_GUARD_END(-1)
+}
+
+int64_t tm_alloc_buffer(int64_t length) {
+  TM_GUARD_BEGIN
+  if (length <= 0)
+    throw TmError(format("buffer length must be positive, got %lld", (long long)length));
+  require_device();
+  auto buf = std::make_shared<Buffer>();
+  hipError_t status = hipMalloc(&buf->ptr, (size_t)length);
+  if (status != hipSuccess) {
+    buf->ptr = nullptr;
+    (void)hipGetLastError();
+    throw TmError(format("could not allocate a %lld-byte device buffer (%s)", (long long)length,
+                         hipGetErrorName(status)));
+  }
+  buf->length = length;
+  return handles().insert(buf);
+  TM_GUARD_END(0)
+}
+
+void *tm_buffer_contents(int64_t buffer) {
+  TM_GUARD_BEGIN
+  return handles().lookup<Buffer>(buffer, Kind::Buffer, "buffer")->ptr;
+  TM_GUARD_END(nullptr)
+}
+
+int64_t tm_buffer_length(int64_t buffer) {
+  TM_GUARD_BEGIN
+  return handles().lookup<Buffer>(buffer, Kind::Buffer, "buffer")->length;
+  TM_GUARD_END(-1)
+}
+
+static int32_t tm_copy(int64_t buffer, int64_t offset, const void *host, int64_t length,
+                       bool to_device) {
+  TM_GUARD_BEGIN
+  if (!host || length < 0 || offset < 0)
+    throw TmError("buffer copy received invalid bounds");
+  auto buf = handles().lookup<Buffer>(buffer, Kind::Buffer, "buffer");
+  if (offset + length > buf->length)
+    throw TmError(format("copy of %lld bytes at offset %lld exceeds the %lld-byte buffer",
+                         (long long)length, (long long)offset, (long long)buf->length));
+  if (length == 0) return 0;
+  Device &dev = require_device();
+  /* Work queued on the library stream is ordered before the copy. */
+  finish(dev.stream);
+  char *dptr = (char *)buf->ptr + offset;
+  if (to_device)
+    hip_check(hipMemcpy(dptr, host, (size_t)length, hipMemcpyHostToDevice), "hipMemcpy");
+  else
+    hip_check(hipMemcpy((void *)host, dptr, (size_t)length, hipMemcpyDeviceToHost), "hipMemcpy");
+  return 0;
+  TM_GUARD_END(-1)
+}
+
+int32_t tm_buffer_write(int64_t buffer, int64_t offset, const void *source, int64_t length) {
+  return tm_copy(buffer, offset, source, length, true);
+}
+
+int32_t tm_buffer_read(int64_t buffer, int64_t offset, void *destination, int64_t length) {
+  return tm_copy(buffer, offset, destination, length, false);
+}
+
+int32_t tm_free_buffer(int64_t buffer) {
+  TM_GUARD_BEGIN
+  if (!handles().remove(buffer, Kind::Buffer))
+    throw TmError(format("buffer handle %lld is not live", (long long)buffer));
+  return 0;
+  TM_GUARD_END(-1)
+}
+
+int32_t tm_launch(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads,
+                  const int32_t *kinds, const int64_t *values, int32_t argc) {
+  TM_GUARD_BEGIN
+  return (int32_t)launch_common(kernel, gx, gy, gz, threads, kinds, values, argc, true, 0,
+                                nullptr);
+  TM_GUARD_END(-1)
+}
+
+int32_t tm_launch_async(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads,
+                        const int32_t *kinds, const int64_t *values, int32_t argc) {
+  TM_GUARD_BEGIN
+  return (int32_t)launch_common(kernel, gx, gy, gz, threads, kinds, values, argc, false, 0,
+                                nullptr);
+  TM_GUARD_END(-1)
+}
+
+int32_t tm_synchronize(void) {
+  TM_GUARD_BEGIN
+  finish(require_device().stream);
+  return 0;
+  TM_GUARD_END(-1)
+}
+
+int32_t tm_launch_timed(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads,
+                        const int32_t *kinds, const int64_t *values, int32_t argc,
+                        int32_t repeats, float *elapsed_ms) {
+  TM_GUARD_BEGIN
+  if (repeats <= 0) throw TmError(format("tm_launch_timed: repeats must be positive, got %d",
+                                         repeats));
+  if (!elapsed_ms) throw TmError("tm_launch_timed received a NULL elapsed_ms");
+  return (int32_t)launch_common(kernel, gx, gy, gz, threads, kinds, values, argc, true, repeats,
+                                elapsed_ms);
+  TM_GUARD_END(-1)
+}
+
+char *tm_kernel_variant(int64_t kernel) {
+  TM_GUARD_BEGIN
+  auto k = handles().lookup<Kernel>(kernel, Kind::Kernel, "kernel");
+  std::lock_guard<std::mutex> guard(k->lock);
+  if (k->last_variant.empty())
+    throw TmError(format("kernel handle %lld has not been launched", (long long)kernel));
+  return dup_string(k->last_variant);
+  TM_GUARD_END(nullptr)
+}
+
+int64_t tm_live_handle_count(void) { return handles().count(); }
+
+}  // extern "C"

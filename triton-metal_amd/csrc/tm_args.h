@@ -1,0 +1,75 @@
+/*
+ * Kernel argument blocks of the built-in gfx950 kernels.
+ *
+ * The host side of tm_launch (runtime.cpp) fills one of these from the
+ * reference-ordered (kinds, values) arrays and passes it to the device function
+ * as its single by-value kernel argument.  The field order follows the
+ * reference's argument lists:
+ *   matmul_kernel        Sources/TritonMetalBench/GEMMKernel.swift:42-45
+ *   attn_fwd             Sources/TritonMetalBench/AttentionKernel.swift:75-78
+ *   attn_bwd_preprocess  Sources/TritonMetalBench/AttentionBackwardKernel.swift:53-64
+ *   attn_bwd_dq          Sources/TritonMetalBench/AttentionBackwardKernel.swift:170-174
+ *   attn_bwd_dkdv        Sources/TritonMetalBench/AttentionBackwardKernel.swift:384-388
+ * followed by what the reference bakes into its IR as compile-time constants
+ * (head_dim) or carries in the grid (heads).
+ */
+#ifndef TM_ARGS_H
+#define TM_ARGS_H
+
+#include <stdint.h>
+
+struct TmGemmArgs {
+  const void *a;
+  const void *b;
+  void *c;
+  int32_t m, n, k;
+  int32_t sam, sak, sbk, sbn, scm, scn;
+};
+
+struct TmAttnFwdArgs {
+  const void *q;
+  const void *k;
+  const void *v;
+  void *o;
+  float *lse; /* may be NULL: the 8-argument form writes no statistics */
+  float sm_scale;
+  int32_t stride_head, stride_seq, n_ctx, stride_lse;
+  int32_t head_dim, heads;
+};
+
+struct TmAttnPreArgs {
+  const void *o;
+  const void *dout;
+  float *delta;
+  int32_t stride_head, stride_seq, stride_lse, n_ctx;
+  int32_t head_dim, heads;
+};
+
+struct TmAttnDqArgs {
+  const void *q;
+  const void *k;
+  const void *v;
+  const void *dout;
+  void *dq;
+  const float *lse;
+  const float *delta;
+  float sm_scale;
+  int32_t stride_head, stride_seq, stride_lse, n_ctx;
+  int32_t head_dim, heads;
+};
+
+struct TmAttnDkdvArgs {
+  const void *q;
+  const void *k;
+  const void *v;
+  const void *dout;
+  void *dk;
+  void *dv;
+  const float *lse;
+  const float *delta;
+  float sm_scale;
+  int32_t stride_head, stride_seq, stride_lse, n_ctx;
+  int32_t head_dim, heads;
+};
+
+#endif

@@ -1,0 +1,216 @@
+"""Host drivers for the dense hot path, over the tm_* C ABI.
+
+These are the reference's own callers restated for the built-in gfx950 kernels:
+  - `matmul` follows python/examples/matmul.py:47-63 (grid (cdiv(M,BM), cdiv(N,BN)),
+    the 12-argument matmul_kernel list);
+  - `AttentionLayer` follows python/examples/attention_training.py:195-247
+    (forward writes O and the log2 logsumexp L; backward runs preprocess, dq,
+    dkdv with the reference's argument lists and grids).
+Every dispatch is a tm_launch (or tm_launch_async) call into the native library.
+"""
+
+import json
+import math
+
+import numpy as np
+
+from . import _core
+from .buffer import DeviceBuffer
+
+_ELEMENTS = {"f32": "float32", "f16": "float16", "bf16": "bfloat16"}
+
+#: Threads per workgroup the reference caller asks for (4 simdgroups of 32).
+REFERENCE_THREADS = 128
+
+
+def cdiv(a, b):
+    return (a + b - 1) // b
+
+
+class BuiltinLibrary:
+    """One built-in library spec and its five kernels, loaded once."""
+
+    NAMES = ("matmul_kernel", "attn_fwd", "attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv")
+
+    def __init__(self, element="f32", head_dim=64, causal=False):
+        if element not in _ELEMENTS:
+            raise ValueError(f"element must be one of {sorted(_ELEMENTS)}")
+        self.element = element
+        self.dtype = _ELEMENTS[element]
+        self.head_dim = head_dim
+        self.causal = causal
+        self.spec = f"builtin element={element} head_dim={head_dim} causal={int(causal)}"
+        self.info = {k["name"]: k for k in json.loads(_core.kernel_info(self.spec))["kernels"]}
+        self.handle = _core.compile_msl(self.spec)
+        self.kernels = {name: _core.load_kernel(self.handle, name) for name in self.NAMES}
+
+    def release(self):
+        for handle in self.kernels.values():
+            _core.release_kernel(handle)
+        self.kernels = {}
+        if self.handle:
+            _core.release_library(self.handle)
+            self.handle = 0
+
+
+_CACHE = {}
+
+
+def library(element="f32", head_dim=64, causal=False) -> BuiltinLibrary:
+    key = (element, head_dim, bool(causal))
+    if key not in _CACHE:
+        _CACHE[key] = BuiltinLibrary(element, head_dim, causal)
+    return _CACHE[key]
+
+
+def _go(kernel, grid, kinds, values, synchronous=True):
+    if synchronous:
+        _core.launch(kernel, grid, REFERENCE_THREADS, kinds, values)
+    else:
+        _core.launch_async(kernel, grid, REFERENCE_THREADS, kinds, values)
+
+
+# --------------------------------------------------------------------------- #
+# GEMM
+# --------------------------------------------------------------------------- #
+
+
+def matmul_args(a, b, c, m, n, k, strides=None, block=(64, 64, 32)):
+    """(grid, kinds, values) of one matmul_kernel dispatch, in the reference's
+    12-argument order (GEMMKernel.swift:42-45).  Default strides: row-major."""
+    sam, sak, sbk, sbn, scm, scn = strides or (k, 1, n, 1, n, 1)
+    grid = (cdiv(m, block[0]), cdiv(n, block[1]), 1)
+    kinds = [_core.ARG_BUFFER] * 3 + [_core.ARG_I32] * 9
+    values = [a.tm_handle, b.tm_handle, c.tm_handle, m, n, k, sam, sak, sbk, sbn, scm, scn]
+    return grid, kinds, values
+
+
+def matmul(a: DeviceBuffer, b: DeviceBuffer, c: DeviceBuffer, m, n, k, strides=None,
+           element=None, synchronous=True):
+    """C = A @ B on the device through matmul_kernel."""
+    element = element or {v: k for k, v in _ELEMENTS.items()}[a.dtype]
+    lib = library(element)
+    grid, kinds, values = matmul_args(a, b, c, m, n, k, strides)
+    _go(lib.kernels["matmul_kernel"], grid, kinds, values, synchronous)
+
+
+def matmul_numpy(a: np.ndarray, b: np.ndarray, element="f32") -> np.ndarray:
+    """Convenience: host arrays in, float32 host array out."""
+    m, k = a.shape
+    k2, n = b.shape
+    assert k == k2
+    dtype = _ELEMENTS[element]
+    bufs = [DeviceBuffer.from_numpy(np.asarray(x, np.float32), dtype) for x in (a, b)]
+    c = DeviceBuffer((m, n), dtype)
+    try:
+        matmul(bufs[0], bufs[1], c, m, n, k, element=element)
+        return c.float32()
+    finally:
+        for x in (*bufs, c):
+            x.free()
+
+
+# --------------------------------------------------------------------------- #
+# Attention
+# --------------------------------------------------------------------------- #
+
+
+class AttentionLayer:
+    """Q, K, V, O, dO, dQ, dK, dV as [heads, seq, dim] device buffers plus the
+    per-row L (log2 logsumexp) and Delta, and the four attention kernels.
+
+    `heads` is batch*heads: the reference's layout [B*H, S, D] with
+    stride_head = S*D and stride_seq = D (AttentionKernel.swift:25-28).
+    """
+
+    def __init__(self, heads, seq, dim, element="f32", causal=False, scale=None,
+                 block_m=16, block_n=32):
+        self.heads, self.seq, self.dim = heads, seq, dim
+        self.element = element
+        self.causal = causal
+        self.block_m, self.block_n = block_m, block_n
+        self.scale = 1.0 / math.sqrt(dim) if scale is None else scale
+        self.lib = library(element, dim, causal)
+        dtype = _ELEMENTS[element]
+        shape = (heads, seq, dim)
+        self.buffers = {name: DeviceBuffer(shape, dtype) for name in
+                        ("q", "k", "v", "o", "do", "dq", "dk", "dv")}
+        self.buffers["lse"] = DeviceBuffer((heads, seq), "float32")
+        self.buffers["delta"] = DeviceBuffer((heads, seq), "float32")
+
+    def free(self):
+        for buffer in self.buffers.values():
+            buffer.free()
+        self.buffers = {}
+
+    def upload(self, name, array):
+        self.buffers[name].write(np.asarray(array, dtype=np.float32)
+                                 if self.element != "f32" else array)
+
+    def read(self, name) -> np.ndarray:
+        return self.buffers[name].float32()
+
+    # -- dispatch descriptions (reference argument lists) ------------------
+
+    def _h(self, name):
+        return self.buffers[name].tm_handle
+
+    def fwd_args(self, stats=True):
+        B, I, F = _core.ARG_BUFFER, _core.ARG_I32, _core.ARG_F32
+        grid = (cdiv(self.seq, self.block_m), self.heads, 1)
+        kinds = [B, B, B, B, F, I, I, I]
+        values = [self._h("q"), self._h("k"), self._h("v"), self._h("o"),
+                  _core.float_bits(self.scale), self.seq * self.dim, self.dim, self.seq]
+        if stats:
+            kinds += [B, I]
+            values += [self._h("lse"), self.seq]
+        return grid, kinds, values
+
+    def pre_args(self):
+        B, I = _core.ARG_BUFFER, _core.ARG_I32
+        grid = (cdiv(self.seq, self.block_m), self.heads, 1)
+        kinds = [B, B, B, I, I, I, I]
+        values = [self._h("o"), self._h("do"), self._h("delta"),
+                  self.seq * self.dim, self.dim, self.seq, self.seq]
+        return grid, kinds, values
+
+    def dq_args(self):
+        B, I, F = _core.ARG_BUFFER, _core.ARG_I32, _core.ARG_F32
+        grid = (cdiv(self.seq, self.block_m), self.heads, 1)
+        kinds = [B] * 7 + [F, I, I, I, I]
+        values = [self._h(x) for x in ("q", "k", "v", "do", "dq", "lse", "delta")] + [
+            _core.float_bits(self.scale), self.seq * self.dim, self.dim, self.seq, self.seq]
+        return grid, kinds, values
+
+    def dkdv_args(self):
+        B, I, F = _core.ARG_BUFFER, _core.ARG_I32, _core.ARG_F32
+        grid = (cdiv(self.seq, self.block_n), self.heads, 1)
+        kinds = [B] * 8 + [F, I, I, I, I]
+        values = [self._h(x) for x in ("q", "k", "v", "do", "dk", "dv", "lse", "delta")] + [
+            _core.float_bits(self.scale), self.seq * self.dim, self.dim, self.seq, self.seq]
+        return grid, kinds, values
+
+    # -- passes --------------------------------------------------------------
+
+    def run_forward(self, synchronous=True, stats=True):
+        _go(self.lib.kernels["attn_fwd"], *self.fwd_args(stats), synchronous=synchronous)
+
+    def run_backward(self, synchronous=True):
+        k = self.lib.kernels
+        _go(k["attn_bwd_preprocess"], *self.pre_args(), synchronous=False)
+        _go(k["attn_bwd_dq"], *self.dq_args(), synchronous=False)
+        _go(k["attn_bwd_dkdv"], *self.dkdv_args(), synchronous=synchronous)
+
+    def forward(self, q, k, v):
+        """Upload, run, return (O, L) as float32 host arrays."""
+        self.upload("q", q)
+        self.upload("k", k)
+        self.upload("v", v)
+        self.run_forward()
+        return self.read("o"), self.read("lse")
+
+    def backward(self, d_out):
+        """Upload dO, run the three backward kernels, return (dQ, dK, dV)."""
+        self.upload("do", d_out)
+        self.run_backward()
+        return self.read("dq"), self.read("dk"), self.read("dv")
