@@ -1,0 +1,287 @@
+/*
+ * Specialised gfx950 FlashAttention-2 kernels for 16-bit element types (bf16,
+ * f16) at head_dim 64 and 128, contiguous head dimension, 16-byte aligned rows.
+ * Same maths and numerics as the generic kernels (and the reference's
+ * AttentionKernel.swift:40-250 / AttentionBackwardKernel.swift): f32 scores,
+ * statistics and accumulators, P rounded to the element type before P V,
+ * exp2 with sm_scale folded into log2(e), L = m + log2(l) in log2 units.
+ *
+ * Forward tiling (one workgroup = 4 waves = 128 queries of one head):
+ *   - each wave owns 32 queries, held in registers as the B operand of
+ *     S^T = K Q^T on v_mfma_f32_16x16x32_{bf16,f16}: a lane then owns one query
+ *     (column l%16) and 4 keys of every 16-key tile, so the row max needs only
+ *     a reduction over the four 16-lane groups and the row sum none until the end;
+ *   - O^T = V^T P^T keeps the lane <-> query ownership, so P goes from the
+ *     softmax straight into the B operand and the rescale is lane-local;
+ *   - K [64 keys][D] and V^T [D][64 keys] are double-buffered in LDS, K in
+ *     16-byte chunks XOR-swizzled by row, V^T in 8-byte units XOR-swizzled by
+ *     row pair, both conflict-free for the MFMA operand reads; V is transposed
+ *     in registers on its way from HBM to LDS;
+ *   - causal: key blocks past the workgroup's last query are never visited,
+ *     waves skip blocks entirely above their queries, masking only runs on
+ *     blocks that straddle the diagonal or n_ctx;
+ *   - the 1-D grid is remapped so that each XCD (workgroups are dealt to the
+ *     8 XCDs round-robin) runs a contiguous range of heads, keeping one head's
+ *     K and V in that XCD's L2; within a head, causal blocks run heaviest first.
+ */
+#include "common.h"
+
+#define TM_NEG_INF (-__builtin_inff())
+
+template <typename T> struct Vec8;
+template <> struct Vec8<bf16_t> { typedef bf16x8 type; };
+template <> struct Vec8<f16_t> { typedef f16x8 type; };
+
+template <typename T>
+TM_DEV typename Vec8<T>::type as_vec8(u32x4 x) {
+  return __builtin_bit_cast(typename Vec8<T>::type, x);
+}
+
+/* Two f32 -> one dword of two 16-bit values (lo first), round to nearest even. */
+template <typename T>
+TM_DEV uint32_t pack2(float lo, float hi) {
+  T a = (T)lo, b = (T)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+/* Workgroup index remapped so consecutive logical ids share an XCD. */
+TM_DEV int xcd_remap(int wg, int nwg) {
+  const int q = nwg >> 3, r = nwg & 7;
+  const int xcd = wg & 7, slot = wg >> 3;
+  return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
+}
+
+
+/* ---- LDS staging ----------------------------------------------------------
+ * K and V tiles are copied HBM -> LDS by global_load_lds_dwordx4, which writes
+ * each lane's 16 bytes to (wave-uniform LDS base) + 16 * lane: one instruction
+ * fills 1 KB.  Rows keep their natural [key][d] order; the 16-byte chunk c of
+ * row r is stored at chunk position c ^ (r & 7), so the 16-row MFMA operand
+ * reads (K: 16 bytes per lane; V: ds_read_b64_tr_b16, 8 bytes per lane) spread
+ * over all banks. */
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+TM_DEV void global_to_lds16(const void *src, char *lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)lds_wave_base, 16, 0, 0);
+}
+
+/* wait for this wave's outstanding vector-memory operations (vmcnt = 0) */
+TM_DEV void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+template <int D>
+TM_DEV int tile_off(int row, int chunk) {
+  return row * (D * 2) + ((chunk ^ (row & 7)) << 4);
+}
+
+/* Copy rows [k0, k0 + ROWS) of a [n, D] tensor (row stride ss elements) into an
+ * LDS tile, the four waves sharing the work.  Rows at or past n are clamped to
+ * row n-1: finite values that the caller masks (scores to -inf, P to 0). */
+template <typename T, int D, int ROWS>
+TM_DEV void stage_rows(const T *src, int64_t ss, int k0, int n, char *tile, int wave, int lane) {
+  constexpr int CPR = D / 8;                      /* 16-byte chunks per row */
+  constexpr int RPI = 64 / CPR;                   /* rows per wave instruction */
+  constexpr int INSTR = ROWS / RPI / 4;           /* instructions per wave */
+  static_assert(INSTR >= 1 && ROWS % (RPI * 4) == 0, "tile rows");
+#pragma unroll
+  for (int i = 0; i < INSTR; ++i) {
+    const int t = wave * INSTR + i;
+    const int row = t * RPI + lane / CPR;
+    const int chunk = (lane % CPR) ^ (row & 7);
+    const int key = min(k0 + row, n - 1);
+    global_to_lds16(src + (int64_t)key * ss + chunk * 8, tile + t * 1024);
+  }
+}
+
+/* A 16x16x32 MFMA operand whose k index runs down the rows of an LDS tile
+ * (the V^T operand of O^T = V^T P^T): lane (c, g) receives rows
+ * r0 + 4g + {0..3} and r0 + 16 + 4g + {0..3} of column d0 + c.
+ * ds_read_b64_tr_b16 gives lane i of a 16-lane group element (i & 3) of the
+ * 8 bytes addressed by lane 4e + (i >> 2), for e = 0..3; so lane j addresses
+ * row r0 + 4g + (j >> 2), columns d0 + 4 (j & 3) .. +3. */
+template <int D>
+TM_DEV u32x4 read_kmajor_operand(const char *tile, int r0, int d0, int g, int c) {
+  const int d = d0 + 4 * (c & 3);
+  const int chunk = d >> 3, half = (d >> 2) & 1;
+  const int ra = r0 + 4 * g + (c >> 2), rb = ra + 16;
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(tile + tile_off<D>(ra, chunk) + (half << 3)));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(tile + tile_off<D>(rb, chunk) + (half << 3)));
+  const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+  return (u32x4){ua[0], ua[1], ub[0], ub[1]};
+}
+
+TM_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+/* ---- forward ------------------------------------------------------------- */
+
+template <typename T, int D, bool CAUSAL>
+TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
+  constexpr int BM = 128, BN = 64, QW = 32;
+  constexpr int KS = D / 32;            /* k-steps of the S^T contraction */
+  constexpr int TILE = BN * D * 2;      /* bytes of one K or V tile */
+  __shared__ __align__(1024) char smem[2][2 * TILE];
+
+  typedef typename Vec8<T>::type v8;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int n = p.n_ctx;
+  const int nqb = (n + BM - 1) / BM;
+  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = logical / nqb;
+  int qb = logical - bh * nqb;
+  if (CAUSAL) qb = nqb - 1 - qb;
+  const int q0 = qb * BM;
+  const int qw0 = q0 + wave * QW;
+  const int64_t base = (int64_t)bh * p.stride_head;
+  const int64_t ss = p.stride_seq;
+  const T *Qg = (const T *)p.q + base;
+  const T *Kg = (const T *)p.k + base;
+  const T *Vg = (const T *)p.v + base;
+  T *Og = (T *)p.o + base;
+
+  const int kend = CAUSAL ? min(n, q0 + BM) : n;
+  const int nblocks = (kend + BN - 1) / BN;
+  if (nblocks > 0) {
+    stage_rows<T, D, BN>(Kg, ss, 0, n, smem[0], wave, lane);
+    stage_rows<T, D, BN>(Vg, ss, 0, n, smem[0] + TILE, wave, lane);
+  }
+
+  /* Q fragments (B operand): query qw0 + qt*16 + c, d = ks*32 + 8g .. +7. */
+  u32x4 qf[2][KS];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qi = min(qw0 + qt * 16 + c, n - 1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[qt][ks] = *(const u32x4 *)(Qg + (int64_t)qi * ss + ks * 32 + 8 * g);
+  }
+
+  const float qk_scale = p.sm_scale * TM_LOG2E;
+  float m_i[2] = {TM_NEG_INF, TM_NEG_INF};
+  float l_i[2] = {0.f, 0.f}; /* per-lane partial sums over this lane's keys */
+  f32x4 acc[D / 16][2];
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) acc[dt][0] = acc[dt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  wait_vmem();
+  __syncthreads();
+
+  for (int j = 0; j < nblocks; ++j) {
+    const int k0 = j * BN;
+    if (j + 1 < nblocks) {
+      char *nxt = smem[(j + 1) & 1];
+      stage_rows<T, D, BN>(Kg, ss, k0 + BN, n, nxt, wave, lane);
+      stage_rows<T, D, BN>(Vg, ss, k0 + BN, n, nxt + TILE, wave, lane);
+    }
+    const bool active = !CAUSAL || k0 <= qw0 + QW - 1;
+    if (active) {
+      const char *kt_ = smem[j & 1];
+      const char *vt_ = smem[j & 1] + TILE;
+      /* S^T = K Q^T: 4 key tiles x 2 query tiles */
+      f32x4 s[4][2];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        s[kt][0] = s[kt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const v8 a = as_vec8<T>(*(const u32x4 *)(kt_ + tile_off<D>(kt * 16 + c, ks * 4 + g)));
+          s[kt][0] = mfma_16x16x32(a, as_vec8<T>(qf[0][ks]), s[kt][0]);
+          s[kt][1] = mfma_16x16x32(a, as_vec8<T>(qf[1][ks]), s[kt][1]);
+        }
+      }
+      const bool edge = (k0 + BN > n) || (CAUSAL && k0 + BN - 1 > qw0);
+      u32x4 pf[2][2]; /* P^T B operand: [query tile][key k-step] */
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const int qi = qw0 + qt * 16 + c;
+        if (edge) {
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int key = k0 + kt * 16 + 4 * g + r;
+              if (key >= n || (CAUSAL && key > qi)) s[kt][qt][r] = TM_NEG_INF;
+            }
+        }
+        float mx = s[0][qt][0];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][qt][r]);
+        mx = group4_max(mx) * qk_scale;
+        const float m_new = fmaxf(m_i[qt], mx);
+        const float alpha = fast_exp2(m_i[qt] - m_new);
+        m_i[qt] = m_new;
+        float rs = 0.f;
+        float pv[4][4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            pv[kt][r] = fast_exp2(__builtin_fmaf(s[kt][qt][r], qk_scale, -m_new));
+            rs += pv[kt][r];
+          }
+        l_i[qt] = l_i[qt] * alpha + rs;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) acc[dt][qt] *= alpha;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          pf[qt][kk][0] = pack2<T>(pv[2 * kk][0], pv[2 * kk][1]);
+          pf[qt][kk][1] = pack2<T>(pv[2 * kk][2], pv[2 * kk][3]);
+          pf[qt][kk][2] = pack2<T>(pv[2 * kk + 1][0], pv[2 * kk + 1][1]);
+          pf[qt][kk][3] = pack2<T>(pv[2 * kk + 1][2], pv[2 * kk + 1][3]);
+        }
+      }
+      /* O^T += V^T P^T */
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const v8 a = as_vec8<T>(read_kmajor_operand<D>(vt_, 32 * kk, dt * 16, g, c));
+          acc[dt][0] = mfma_16x16x32(a, as_vec8<T>(pf[0][kk]), acc[dt][0]);
+          acc[dt][1] = mfma_16x16x32(a, as_vec8<T>(pf[1][kk]), acc[dt][1]);
+        }
+      }
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+
+  /* epilogue: O = acc / l, L = m + log2(l) */
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qi = qw0 + qt * 16 + c;
+    const float l = group4_sum(l_i[qt]);
+    if (qi < n) {
+      const float inv = 1.f / l;
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+        u32x2 w;
+        w[0] = pack2<T>(acc[dt][qt][0] * inv, acc[dt][qt][1] * inv);
+        w[1] = pack2<T>(acc[dt][qt][2] * inv, acc[dt][qt][3] * inv);
+        *(u32x2 *)(Og + (int64_t)qi * ss + dt * 16 + 4 * g) = w;
+      }
+      if (p.lse && g == 0) p.lse[(int64_t)bh * p.stride_lse + qi] = m_i[qt] + log2f(l);
+    }
+  }
+}
+
+#define TM_FWD_FAST(T, TN, D, CAUSAL, CN)                                                     \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void  \
+  tm_attn_fwd_fast_##TN##_d##D##CN(TmAttnFwdArgs p) {                                         \
+    attn_fwd_fast<T, D, CAUSAL>(p);                                                           \
+  }                                                                                           \
+  extern "C" __global__ __launch_bounds__(256) void tm_attn_fwd_fast1_##TN##_d##D##CN(        \
+      TmAttnFwdArgs p) {                                                                      \
+    attn_fwd_fast<T, D, CAUSAL>(p);                                                           \
+  }
+#define TM_FWD_FAST_ALL(T, TN)           \
+  TM_FWD_FAST(T, TN, 64, false, )        \
+  TM_FWD_FAST(T, TN, 64, true, _causal)  \
+  TM_FWD_FAST(T, TN, 128, false, )       \
+  TM_FWD_FAST(T, TN, 128, true, _causal)
+TM_FWD_FAST_ALL(bf16_t, bf16)
+TM_FWD_FAST_ALL(f16_t, f16)

@@ -481,6 +481,25 @@ void check_signature(const BuiltinInfo &info, const std::vector<Arg> &args) {
                            kind_names[info.kinds[i]], info.kinds[i], args[i].kind));
 }
 
+/* TRITON_METAL_GENERIC=1 keeps every dispatch on the generic kernels (for A/B
+ * comparisons of the specialised ones). */
+bool fast_paths_enabled() {
+  static const bool enabled = [] {
+    const char *v = getenv("TRITON_METAL_GENERIC");
+    return !(v && *v && strcmp(v, "0") != 0);
+  }();
+  return enabled;
+}
+
+/* The specialised attention kernels need a 16-bit element type, head_dim 64
+ * or 128, 16-byte aligned rows and a positive finite scale. */
+bool attn_fast_ok(const BuiltinSpec &spec, int32_t stride_head, int32_t stride_seq,
+                  float sm_scale) {
+  return fast_paths_enabled() && spec.element != Element::F32 &&
+         (spec.head_dim == 64 || spec.head_dim == 128) && stride_seq % 8 == 0 &&
+         stride_head % 8 == 0 && std::isfinite(sm_scale) && sm_scale > 0.f;
+}
+
 int padded_head_dim(int d) { return d <= 32 ? 32 : d <= 64 ? 64 : d <= 96 ? 96 : 128; }
 
 std::string attn_symbol(const char *op, const BuiltinSpec &spec) {
@@ -579,9 +598,16 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         plan.empty = true;
         return plan;
       }
-      plan.variant = attn_symbol("fwd", spec);
-      plan.grid[0] = (unsigned)cdiv(p.n_ctx, 64);
-      plan.grid[1] = (unsigned)heads;
+      if (attn_fast_ok(spec, p.stride_head, p.stride_seq, p.sm_scale)) {
+        const char *tag = getenv("TRITON_METAL_FWD_TAG");
+        plan.variant = format("tm_attn_fwd_%s_%s_d%d%s", tag ? tag : "fast", el, spec.head_dim,
+                              spec.causal ? "_causal" : "");
+        plan.grid[0] = (unsigned)(cdiv(p.n_ctx, 128) * heads);
+      } else {
+        plan.variant = attn_symbol("fwd", spec);
+        plan.grid[0] = (unsigned)cdiv(p.n_ctx, 64);
+        plan.grid[1] = (unsigned)heads;
+      }
       plan.block = 256;
       set_kernarg(plan, p);
       break;
