@@ -26,6 +26,8 @@
  */
 #include "common.h"
 
+#include <type_traits>
+
 #define TM_NEG_INF (-__builtin_inff())
 
 template <typename T> struct Vec8;
@@ -38,10 +40,11 @@ TM_DEV typename Vec8<T>::type as_vec8(u32x4 x) {
 }
 
 /* Two f32 -> one dword of two 16-bit values (lo first), round to nearest even. */
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 template <typename T>
 TM_DEV uint32_t pack2(float lo, float hi) {
-  T a = (T)lo, b = (T)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  typedef T t2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, t2));
 }
 
 /* Workgroup index remapped so consecutive logical ids share an XCD. */
@@ -70,9 +73,23 @@ TM_DEV void global_to_lds16(const void *src, char *lds_wave_base) {
 /* wait for this wave's outstanding vector-memory operations (vmcnt = 0) */
 TM_DEV void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+/* 16-byte chunk position of logical chunk `chunk` in row `row`.  The XOR key
+ * makes both operand read patterns conflict-free: 16 consecutive rows at one
+ * chunk (ds_read_b128) and 8 consecutive rows at a chunk pair
+ * (ds_read_b64_tr_b16).  D = 128: rows are 256 bytes, the key spreads 16 rows
+ * over the 16 chunk positions with even keys for rows 0-7 of each group of 16;
+ * D = 64: rows are 128 bytes, row parity picks the half, the key spreads each
+ * parity class the same way. */
+template <int D>
+TM_DEV int swz(int row) {
+  if (D == 128) return ((row & 7) << 1) | ((row >> 3) & 1);
+  const int t = row >> 1;
+  return ((t & 3) << 1) | ((t >> 2) & 1);
+}
+
 template <int D>
 TM_DEV int tile_off(int row, int chunk) {
-  return row * (D * 2) + ((chunk ^ (row & 7)) << 4);
+  return row * (D * 2) + ((chunk ^ swz<D>(row)) << 4);
 }
 
 /* Copy rows [k0, k0 + ROWS) of a [n, D] tensor (row stride ss elements) into an
@@ -88,7 +105,7 @@ TM_DEV void stage_rows(const T *src, int64_t ss, int k0, int n, char *tile, int 
   for (int i = 0; i < INSTR; ++i) {
     const int t = wave * INSTR + i;
     const int row = t * RPI + lane / CPR;
-    const int chunk = (lane % CPR) ^ (row & 7);
+    const int chunk = (lane % CPR) ^ swz<D>(row);
     const int key = min(k0 + row, n - 1);
     global_to_lds16(src + (int64_t)key * ss + chunk * 8, tile + t * 1024);
   }
@@ -122,7 +139,11 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   constexpr int BM = 128, BN = 64, QW = 32;
   constexpr int KS = D / 32;            /* k-steps of the S^T contraction */
   constexpr int TILE = BN * D * 2;      /* bytes of one K or V tile */
-  __shared__ __align__(1024) char smem[2][2 * TILE];
+  /* Two separate arrays (not one [2][...]) so the compiler can tell the
+   * prefetch's LDS writes from the current tile's reads and does not wait for
+   * the prefetch before reading. */
+  __shared__ __align__(1024) char lds_a[2 * TILE];
+  __shared__ __align__(1024) char lds_b[2 * TILE];
 
   typedef typename Vec8<T>::type v8;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -145,8 +166,8 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   const int kend = CAUSAL ? min(n, q0 + BM) : n;
   const int nblocks = (kend + BN - 1) / BN;
   if (nblocks > 0) {
-    stage_rows<T, D, BN>(Kg, ss, 0, n, smem[0], wave, lane);
-    stage_rows<T, D, BN>(Vg, ss, 0, n, smem[0] + TILE, wave, lane);
+    stage_rows<T, D, BN>(Kg, ss, 0, n, lds_a, wave, lane);
+    stage_rows<T, D, BN>(Vg, ss, 0, n, lds_a + TILE, wave, lane);
   }
 
   /* Q fragments (B operand): query qw0 + qt*16 + c, d = ks*32 + 8g .. +7. */
@@ -169,17 +190,15 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   wait_vmem();
   __syncthreads();
 
-  for (int j = 0; j < nblocks; ++j) {
+  /* One key block: prefetch block j+1 into `nxt`, compute block j from `cur`. */
+  auto step = [&](const char *cur, char *nxt, int j) {
     const int k0 = j * BN;
     if (j + 1 < nblocks) {
-      char *nxt = smem[(j + 1) & 1];
       stage_rows<T, D, BN>(Kg, ss, k0 + BN, n, nxt, wave, lane);
       stage_rows<T, D, BN>(Vg, ss, k0 + BN, n, nxt + TILE, wave, lane);
     }
     const bool active = !CAUSAL || k0 <= qw0 + QW - 1;
     if (active) {
-      const char *kt_ = smem[j & 1];
-      const char *vt_ = smem[j & 1] + TILE;
       /* S^T = K Q^T: 4 key tiles x 2 query tiles */
       f32x4 s[4][2];
 #pragma unroll
@@ -187,13 +206,14 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
         s[kt][0] = s[kt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          const v8 a = as_vec8<T>(*(const u32x4 *)(kt_ + tile_off<D>(kt * 16 + c, ks * 4 + g)));
+          const v8 a = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D>(kt * 16 + c, ks * 4 + g)));
           s[kt][0] = mfma_16x16x32(a, as_vec8<T>(qf[0][ks]), s[kt][0]);
           s[kt][1] = mfma_16x16x32(a, as_vec8<T>(qf[1][ks]), s[kt][1]);
         }
       }
       const bool edge = (k0 + BN > n) || (CAUSAL && k0 + BN - 1 > qw0);
       u32x4 pf[2][2]; /* P^T B operand: [query tile][key k-step] */
+      float alpha[2];
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
         const int qi = qw0 + qt * 16 + c;
@@ -213,7 +233,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
           for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][qt][r]);
         mx = group4_max(mx) * qk_scale;
         const float m_new = fmaxf(m_i[qt], mx);
-        const float alpha = fast_exp2(m_i[qt] - m_new);
+        alpha[qt] = fast_exp2(m_i[qt] - m_new);
         m_i[qt] = m_new;
         float rs = 0.f;
         float pv[4][4];
@@ -224,9 +244,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
             pv[kt][r] = fast_exp2(__builtin_fmaf(s[kt][qt][r], qk_scale, -m_new));
             rs += pv[kt][r];
           }
-        l_i[qt] = l_i[qt] * alpha + rs;
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) acc[dt][qt] *= alpha;
+        l_i[qt] = l_i[qt] * alpha[qt] + rs;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           pf[qt][kk][0] = pack2<T>(pv[2 * kk][0], pv[2 * kk][1]);
@@ -235,12 +253,18 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
           pf[qt][kk][3] = pack2<T>(pv[2 * kk + 1][2], pv[2 * kk + 1][3]);
         }
       }
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+        acc[dt][0] *= alpha[0];
+        acc[dt][1] *= alpha[1];
+      }
       /* O^T += V^T P^T */
+      const char *vt = cur + TILE;
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) {
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          const v8 a = as_vec8<T>(read_kmajor_operand<D>(vt_, 32 * kk, dt * 16, g, c));
+          const v8 a = as_vec8<T>(read_kmajor_operand<D>(vt, 32 * kk, dt * 16, g, c));
           acc[dt][0] = mfma_16x16x32(a, as_vec8<T>(pf[0][kk]), acc[dt][0]);
           acc[dt][1] = mfma_16x16x32(a, as_vec8<T>(pf[1][kk]), acc[dt][1]);
         }
@@ -248,6 +272,11 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
     }
     wait_vmem();
     __syncthreads();
+  };
+
+  for (int j = 0; j < nblocks; j += 2) {
+    step(lds_a, lds_b, j);
+    if (j + 1 < nblocks) step(lds_b, lds_a, j + 1);
   }
 
   /* epilogue: O = acc / l, L = m + log2(l) */
@@ -269,13 +298,346 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   }
 }
 
+/* ---- backward: dQ ------------------------------------------------------
+ * One workgroup = 4 waves = 128 queries; each wave owns 32 queries and walks
+ * the key blocks (64 keys) of its head.  Per block, with the lane owning one
+ * query as in the forward:
+ *   S^T  = K Q^T, dP^T = V dO^T            (K, V: ds_read_b128 of the tiles)
+ *   P^T  = exp2(qk_scale S^T - L), dS^T = P^T (dP^T - Delta)
+ *   dQ^T += K^T dS^T                       (K^T: ds_read_b64_tr_b16 of the K tile)
+ * dS is rounded to the element type before its dot, as the reference does
+ * (AttentionBackwardKernel.swift:155-160). */
+template <typename T, int D, bool CAUSAL>
+TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
+  constexpr int BM = 128, BN = 64, QW = 32;
+  constexpr int KS = D / 32;
+  constexpr int TILE = BN * D * 2;
+  __shared__ __align__(1024) char lds_a[2 * TILE];
+  __shared__ __align__(1024) char lds_b[2 * TILE];
+
+  typedef typename Vec8<T>::type v8;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int n = p.n_ctx;
+  const int nqb = (n + BM - 1) / BM;
+  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = logical / nqb;
+  int qb = logical - bh * nqb;
+  if (CAUSAL) qb = nqb - 1 - qb;
+  const int q0 = qb * BM;
+  const int qw0 = q0 + wave * QW;
+  const int64_t base = (int64_t)bh * p.stride_head;
+  const int64_t ss = p.stride_seq;
+  const T *Qg = (const T *)p.q + base;
+  const T *Kg = (const T *)p.k + base;
+  const T *Vg = (const T *)p.v + base;
+  const T *dOg = (const T *)p.dout + base;
+  T *dQg = (T *)p.dq + base;
+  const float *Lg = p.lse + (int64_t)bh * p.stride_lse;
+  const float *Dg = p.delta + (int64_t)bh * p.stride_lse;
+
+  const int kend = CAUSAL ? min(n, q0 + BM) : n;
+  const int nblocks = (kend + BN - 1) / BN;
+  if (nblocks > 0) {
+    stage_rows<T, D, BN>(Kg, ss, 0, n, lds_a, wave, lane);
+    stage_rows<T, D, BN>(Vg, ss, 0, n, lds_a + TILE, wave, lane);
+  }
+
+  u32x4 qf[2][KS], df[2][KS];
+  float lse[2], dlt[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qi = min(qw0 + qt * 16 + c, n - 1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[qt][ks] = *(const u32x4 *)(Qg + (int64_t)qi * ss + ks * 32 + 8 * g);
+      df[qt][ks] = *(const u32x4 *)(dOg + (int64_t)qi * ss + ks * 32 + 8 * g);
+    }
+    lse[qt] = Lg[qi];
+    dlt[qt] = Dg[qi];
+  }
+  const float qk_scale = p.sm_scale * TM_LOG2E;
+  f32x4 acc[D / 16][2];
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) acc[dt][0] = acc[dt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  wait_vmem();
+  __syncthreads();
+
+  auto step = [&](const char *cur, char *nxt, int j) {
+    const int k0 = j * BN;
+    if (j + 1 < nblocks) {
+      stage_rows<T, D, BN>(Kg, ss, k0 + BN, n, nxt, wave, lane);
+      stage_rows<T, D, BN>(Vg, ss, k0 + BN, n, nxt + TILE, wave, lane);
+    }
+    const bool active = !CAUSAL || k0 <= qw0 + QW - 1;
+    if (active) {
+      f32x4 s[4][2], dp[4][2];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        s[kt][0] = s[kt][1] = dp[kt][0] = dp[kt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const v8 ka = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D>(kt * 16 + c, ks * 4 + g)));
+          const v8 va =
+              as_vec8<T>(*(const u32x4 *)(cur + TILE + tile_off<D>(kt * 16 + c, ks * 4 + g)));
+          s[kt][0] = mfma_16x16x32(ka, as_vec8<T>(qf[0][ks]), s[kt][0]);
+          s[kt][1] = mfma_16x16x32(ka, as_vec8<T>(qf[1][ks]), s[kt][1]);
+          dp[kt][0] = mfma_16x16x32(va, as_vec8<T>(df[0][ks]), dp[kt][0]);
+          dp[kt][1] = mfma_16x16x32(va, as_vec8<T>(df[1][ks]), dp[kt][1]);
+        }
+      }
+      const bool edge = (k0 + BN > n) || (CAUSAL && k0 + BN - 1 > qw0);
+      u32x4 dsf[2][2];
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const int qi = qw0 + qt * 16 + c;
+        float ds[4][4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float x = __builtin_fmaf(s[kt][qt][r], qk_scale, -lse[qt]);
+            if (edge) {
+              const int key = k0 + kt * 16 + 4 * g + r;
+              if (key >= n || (CAUSAL && key > qi)) x = TM_NEG_INF;
+            }
+            ds[kt][r] = fast_exp2(x) * (dp[kt][qt][r] - dlt[qt]);
+          }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          dsf[qt][kk][0] = pack2<T>(ds[2 * kk][0], ds[2 * kk][1]);
+          dsf[qt][kk][1] = pack2<T>(ds[2 * kk][2], ds[2 * kk][3]);
+          dsf[qt][kk][2] = pack2<T>(ds[2 * kk + 1][0], ds[2 * kk + 1][1]);
+          dsf[qt][kk][3] = pack2<T>(ds[2 * kk + 1][2], ds[2 * kk + 1][3]);
+        }
+      }
+      /* dQ^T += K^T dS^T */
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const v8 a = as_vec8<T>(read_kmajor_operand<D>(cur, 32 * kk, dt * 16, g, c));
+          acc[dt][0] = mfma_16x16x32(a, as_vec8<T>(dsf[0][kk]), acc[dt][0]);
+          acc[dt][1] = mfma_16x16x32(a, as_vec8<T>(dsf[1][kk]), acc[dt][1]);
+        }
+      }
+    }
+    wait_vmem();
+    __syncthreads();
+  };
+
+  for (int j = 0; j < nblocks; j += 2) {
+    step(lds_a, lds_b, j);
+    if (j + 1 < nblocks) step(lds_b, lds_a, j + 1);
+  }
+
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qi = qw0 + qt * 16 + c;
+    if (qi < n) {
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+        u32x2 w;
+        w[0] = pack2<T>(acc[dt][qt][0] * p.sm_scale, acc[dt][qt][1] * p.sm_scale);
+        w[1] = pack2<T>(acc[dt][qt][2] * p.sm_scale, acc[dt][qt][3] * p.sm_scale);
+        *(u32x2 *)(dQg + (int64_t)qi * ss + dt * 16 + 4 * g) = w;
+      }
+    }
+  }
+}
+
+/* ---- backward: dK, dV ---------------------------------------------------
+ * One workgroup = 4 waves = 128 keys; each wave owns 32 keys, held in
+ * registers (K^T and V^T as B operands), and walks the query blocks (32
+ * queries) of its head.  Per block, with the lane owning one key:
+ *   S  = Q K^T, dP = dO V^T                (Q, dO: ds_read_b128 of the tiles)
+ *   P  = exp2(qk_scale S - L), dS = P (dP - Delta)
+ *   dV^T += dO^T P, dK^T += Q^T dS         (dO^T, Q^T: ds_read_b64_tr_b16)
+ * P and dS are rounded to the element type before their dots
+ * (AttentionBackwardKernel.swift:357-369).  Causal: the heaviest key blocks
+ * (lowest keys) run first and the query walk starts at the block's first key. */
+template <typename T, int D, bool CAUSAL>
+TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
+  constexpr int BN = 128, KW = 32, BM = 32;
+  constexpr int KS = D / 32;
+  constexpr int TILE = BM * D * 2;
+  __shared__ __align__(1024) char lds_a[2 * TILE];
+  __shared__ __align__(1024) char lds_b[2 * TILE];
+
+  typedef typename Vec8<T>::type v8;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int n = p.n_ctx;
+  const int nkb = (n + BN - 1) / BN;
+  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = logical / nkb;
+  const int kb = logical - bh * nkb;
+  const int k0 = kb * BN;
+  const int kw0 = k0 + wave * KW;
+  const int64_t base = (int64_t)bh * p.stride_head;
+  const int64_t ss = p.stride_seq;
+  const T *Qg = (const T *)p.q + base;
+  const T *Kg = (const T *)p.k + base;
+  const T *Vg = (const T *)p.v + base;
+  const T *dOg = (const T *)p.dout + base;
+  T *dKg = (T *)p.dk + base;
+  T *dVg = (T *)p.dv + base;
+  const float *Lg = p.lse + (int64_t)bh * p.stride_lse;
+  const float *Dg = p.delta + (int64_t)bh * p.stride_lse;
+
+  const int q_start = CAUSAL ? k0 : 0;
+  const int nblocks = (n - q_start + BM - 1) / BM;
+  if (nblocks > 0) {
+    stage_rows<T, D, BM>(Qg, ss, q_start, n, lds_a, wave, lane);
+    stage_rows<T, D, BM>(dOg, ss, q_start, n, lds_a + TILE, wave, lane);
+  }
+
+  u32x4 kf[2][KS], vf[2][KS];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    const int key = min(kw0 + kt * 16 + c, n - 1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kf[kt][ks] = *(const u32x4 *)(Kg + (int64_t)key * ss + ks * 32 + 8 * g);
+      vf[kt][ks] = *(const u32x4 *)(Vg + (int64_t)key * ss + ks * 32 + 8 * g);
+    }
+  }
+  const float qk_scale = p.sm_scale * TM_LOG2E;
+  f32x4 dk[D / 16][2], dv[D / 16][2];
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt)
+    dk[dt][0] = dk[dt][1] = dv[dt][0] = dv[dt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  wait_vmem();
+  __syncthreads();
+
+  auto step = [&](const char *cur, char *nxt, int i) {
+    const int qs = q_start + i * BM;
+    if (i + 1 < nblocks) {
+      stage_rows<T, D, BM>(Qg, ss, qs + BM, n, nxt, wave, lane);
+      stage_rows<T, D, BM>(dOg, ss, qs + BM, n, nxt + TILE, wave, lane);
+    }
+    const bool active = !CAUSAL || qs + BM - 1 >= kw0;
+    if (active) {
+      /* L and Delta of queries qs + qt*16 + 4g + {0..3} */
+      f32x4 lse[2], dlt[2];
+      if (qs + BM <= n) {
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+          lse[qt] = *(const f32x4 *)(Lg + qs + qt * 16 + 4 * g);
+          dlt[qt] = *(const f32x4 *)(Dg + qs + qt * 16 + 4 * g);
+        }
+      } else {
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int qi = min(qs + qt * 16 + 4 * g + r, n - 1);
+            lse[qt][r] = Lg[qi];
+            dlt[qt][r] = Dg[qi];
+          }
+      }
+      f32x4 s[2][2], dp[2][2];
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        s[0][qt] = s[1][qt] = dp[0][qt] = dp[1][qt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const v8 qa = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D>(qt * 16 + c, ks * 4 + g)));
+          const v8 da =
+              as_vec8<T>(*(const u32x4 *)(cur + TILE + tile_off<D>(qt * 16 + c, ks * 4 + g)));
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) {
+            s[kt][qt] = mfma_16x16x32(qa, as_vec8<T>(kf[kt][ks]), s[kt][qt]);
+            dp[kt][qt] = mfma_16x16x32(da, as_vec8<T>(vf[kt][ks]), dp[kt][qt]);
+          }
+        }
+      }
+      const bool edge = (qs + BM > n) || (CAUSAL && qs < kw0 + KW - 1);
+      u32x4 pf[2], dsf[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const int key = kw0 + kt * 16 + c;
+        float pr[2][4], ds[2][4];
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float x = __builtin_fmaf(s[kt][qt][r], qk_scale, -lse[qt][r]);
+            if (edge) {
+              const int qi = qs + qt * 16 + 4 * g + r;
+              if (qi >= n || (CAUSAL && qi < key)) x = TM_NEG_INF;
+            }
+            pr[qt][r] = fast_exp2(x);
+            ds[qt][r] = pr[qt][r] * (dp[kt][qt][r] - dlt[qt][r]);
+          }
+        pf[kt] = (u32x4){pack2<T>(pr[0][0], pr[0][1]), pack2<T>(pr[0][2], pr[0][3]),
+                         pack2<T>(pr[1][0], pr[1][1]), pack2<T>(pr[1][2], pr[1][3])};
+        dsf[kt] = (u32x4){pack2<T>(ds[0][0], ds[0][1]), pack2<T>(ds[0][2], ds[0][3]),
+                          pack2<T>(ds[1][0], ds[1][1]), pack2<T>(ds[1][2], ds[1][3])};
+      }
+      /* dV^T += dO^T P, dK^T += Q^T dS */
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+        const v8 doa = as_vec8<T>(read_kmajor_operand<D>(cur + TILE, 0, dt * 16, g, c));
+        const v8 qa = as_vec8<T>(read_kmajor_operand<D>(cur, 0, dt * 16, g, c));
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          dv[dt][kt] = mfma_16x16x32(doa, as_vec8<T>(pf[kt]), dv[dt][kt]);
+          dk[dt][kt] = mfma_16x16x32(qa, as_vec8<T>(dsf[kt]), dk[dt][kt]);
+        }
+      }
+    }
+    wait_vmem();
+    __syncthreads();
+  };
+
+  for (int i = 0; i < nblocks; i += 2) {
+    step(lds_a, lds_b, i);
+    if (i + 1 < nblocks) step(lds_b, lds_a, i + 1);
+  }
+
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    const int key = kw0 + kt * 16 + c;
+    if (key < n) {
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+        u32x2 wk, wv;
+        wk[0] = pack2<T>(dk[dt][kt][0] * p.sm_scale, dk[dt][kt][1] * p.sm_scale);
+        wk[1] = pack2<T>(dk[dt][kt][2] * p.sm_scale, dk[dt][kt][3] * p.sm_scale);
+        wv[0] = pack2<T>(dv[dt][kt][0], dv[dt][kt][1]);
+        wv[1] = pack2<T>(dv[dt][kt][2], dv[dt][kt][3]);
+        *(u32x2 *)(dKg + (int64_t)key * ss + dt * 16 + 4 * g) = wk;
+        *(u32x2 *)(dVg + (int64_t)key * ss + dt * 16 + 4 * g) = wv;
+      }
+    }
+  }
+}
+
+#define TM_BWD_FAST(T, TN, D, CAUSAL, CN)                                                     \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void  \
+  tm_attn_dq_fast_##TN##_d##D##CN(TmAttnDqArgs p) {                                           \
+    attn_dq_fast<T, D, CAUSAL>(p);                                                            \
+  }                                                                                           \
+  /* dK, dV accumulators (128 registers) plus the wave's K^T and V^T fragments do   \
+   * not fit in 256 registers: one wave per SIMD, accumulators in AGPRs. */               \
+  extern "C" __global__ __launch_bounds__(256) void tm_attn_dkdv_fast_##TN##_d##D##CN(        \
+      TmAttnDkdvArgs p) {                                                                     \
+    attn_dkdv_fast<T, D, CAUSAL>(p);                                                          \
+  }
+#define TM_BWD_FAST_ALL(T, TN)           \
+  TM_BWD_FAST(T, TN, 64, false, )        \
+  TM_BWD_FAST(T, TN, 64, true, _causal)  \
+  TM_BWD_FAST(T, TN, 128, false, )       \
+  TM_BWD_FAST(T, TN, 128, true, _causal)
+TM_BWD_FAST_ALL(bf16_t, bf16)
+TM_BWD_FAST_ALL(f16_t, f16)
+
 #define TM_FWD_FAST(T, TN, D, CAUSAL, CN)                                                     \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void  \
   tm_attn_fwd_fast_##TN##_d##D##CN(TmAttnFwdArgs p) {                                         \
-    attn_fwd_fast<T, D, CAUSAL>(p);                                                           \
-  }                                                                                           \
-  extern "C" __global__ __launch_bounds__(256) void tm_attn_fwd_fast1_##TN##_d##D##CN(        \
-      TmAttnFwdArgs p) {                                                                      \
     attn_fwd_fast<T, D, CAUSAL>(p);                                                           \
   }
 #define TM_FWD_FAST_ALL(T, TN)           \

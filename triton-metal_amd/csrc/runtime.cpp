@@ -671,8 +671,16 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         plan.empty = true;
         return plan;
       }
-      plan.grid[0] = (unsigned)cdiv(n_ctx, 64);
-      plan.grid[1] = (unsigned)heads;
+      const bool fast = attn_fast_ok(spec, stride_head, stride_seq, sm_scale) && stride_lse % 4 == 0;
+      if (fast) {
+        plan.grid[0] = (unsigned)(cdiv(n_ctx, 128) * heads);
+      } else {
+        plan.grid[0] = (unsigned)cdiv(n_ctx, 64);
+        plan.grid[1] = (unsigned)heads;
+      }
+      const std::string fast_name =
+          format("tm_attn_%s_fast_%s_d%d%s", dq ? "dq" : "dkdv", el, spec.head_dim,
+                 spec.causal ? "_causal" : "");
       plan.block = 256;
       if (dq) {
         TmAttnDqArgs p{};
@@ -690,7 +698,7 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         p.n_ctx = n_ctx;
         p.head_dim = spec.head_dim;
         p.heads = (int32_t)heads;
-        plan.variant = attn_symbol("dq", spec);
+        plan.variant = fast ? fast_name : attn_symbol("dq", spec);
         set_kernarg(plan, p);
       } else {
         TmAttnDkdvArgs p{};
@@ -709,7 +717,7 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         p.n_ctx = n_ctx;
         p.head_dim = spec.head_dim;
         p.heads = (int32_t)heads;
-        plan.variant = attn_symbol("dkdv", spec);
+        plan.variant = fast ? fast_name : attn_symbol("dkdv", spec);
         set_kernarg(plan, p);
       }
       break;
