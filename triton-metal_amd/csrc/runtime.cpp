@@ -378,7 +378,7 @@ struct Published {
 
 Published published_shape(Builtin id) {
   switch (id) {
-    case Builtin::Matmul: return {256, {64, 64}};
+    case Builtin::Matmul: return {256, {64, 64}}; /* 512 threads, 256 x 256 on the fast path */
     case Builtin::AttnFwd: return {256, {64}};
     case Builtin::AttnPre: return {256, {64}};
     case Builtin::AttnDq: return {256, {64}};
@@ -559,10 +559,22 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         plan.empty = true;
         return plan;
       }
-      plan.variant = format("tm_gemm_generic_%s", el);
-      plan.grid[0] = (unsigned)cdiv(p.m, 64);
-      plan.grid[1] = (unsigned)cdiv(p.n, 64);
-      plan.block = 256;
+      /* The specialised kernel: 16-bit elements, row-major operands with unit
+       * inner stride and 16-byte aligned rows, 256 x 256 x 64 tiles. */
+      const bool fast = fast_paths_enabled() && spec.element != Element::F32 && p.sak == 1 &&
+                        p.sbn == 1 && p.scn == 1 && p.m % 256 == 0 && p.n % 256 == 0 &&
+                        p.k % 64 == 0 && p.k > 0 && p.sam % 8 == 0 && p.sbk % 8 == 0 &&
+                        p.scm % 8 == 0;
+      if (fast) {
+        plan.variant = format("tm_gemm_fast_%s", el);
+        plan.grid[0] = (unsigned)((p.m / 256) * (p.n / 256));
+        plan.block = 512;
+      } else {
+        plan.variant = format("tm_gemm_generic_%s", el);
+        plan.grid[0] = (unsigned)cdiv(p.m, 64);
+        plan.grid[1] = (unsigned)cdiv(p.n, 64);
+        plan.block = 256;
+      }
       set_kernarg(plan, p);
       break;
     }
