@@ -1024,7 +1024,8 @@ char *tm_unusable_reason(void) {
 char *tm_device_name(void) {
   Device &dev = device();
   if (!dev.present) return nullptr;
-  return dup_string(dev.name + " (" + dev.arch + ")");
+  return dup_string(dev.name.empty() ? "AMD GPU (" + dev.arch + ")"
+                                     : dev.name + " (" + dev.arch + ")");
 }
 
 char *tm_emit_msl(const char *module, int32_t num_simdgroups) {
