@@ -44,10 +44,11 @@ METRIC = "FA2 fwd/bwd TFLOP/s (b4 h32 s4096 d128 bf16) + GEMM TFLOP/s, % MFMA pe
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--kernel-repeats", type=int, default=10,
-                    help="back-to-back dispatches per HIP-event timing of one kernel")
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sample-ms", type=float, default=25.0,
+                    help="GPU time per timing sample of one kernel (the reference packs "
+                         "dispatches into ~25 ms samples and takes the median of 3)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the baseline sample")
@@ -105,12 +106,21 @@ def normal_bf16(shape, seed):
     return bf16_bits(rng.standard_normal(shape, dtype=np.float32))
 
 
-def kernel_ms(core, kernel, grid, kinds, values, repeats):
-    """Average duration of one dispatch, from HIP events around `repeats`."""
-    return core.launch_timed(kernel, grid, 128, kinds, values, repeats) / repeats
+def kernel_ms(core, kernel, grid, kinds, values, sample_ms):
+    """Average duration of one dispatch, the reference's way
+    (Sources/TritonMetalBench/GEMMBenchmark.swift:250-277): a calibration run
+    sizes a sample of about `sample_ms` of back-to-back dispatches, a warm-up of
+    four samples' worth settles the clocks, and the median of 3 samples timed
+    with HIP events on the library stream is reported."""
+    probe = core.launch_timed(kernel, grid, 128, kinds, values, 4) / 4
+    repeats = max(4, int(sample_ms / max(probe, 1e-3)))
+    core.launch_timed(kernel, grid, 128, kinds, values, 4 * repeats)
+    samples = sorted(core.launch_timed(kernel, grid, 128, kinds, values, repeats) / repeats
+                     for _ in range(3))
+    return samples[1]
 
 
-def bench_attention(core, ops, batch, heads, seq, dim, causal, steps, warmup, repeats,
+def bench_attention(core, ops, batch, heads, seq, dim, causal, steps, warmup, sample_ms,
                     backward=True):
     bh = batch * heads
     layer = ops.AttentionLayer(bh, seq, dim, "bf16", causal)
@@ -140,7 +150,7 @@ def bench_attention(core, ops, batch, heads, seq, dim, causal, steps, warmup, re
         per_kernel = {}
         for name, (grid, kinds, values) in launches:
             per_kernel[name] = {
-                "ms": kernel_ms(core, kern[name], grid, kinds, values, repeats),
+                "ms": kernel_ms(core, kern[name], grid, kinds, values, sample_ms),
                 "variant": core.kernel_variant(kern[name]),
             }
     finally:
@@ -148,7 +158,7 @@ def bench_attention(core, ops, batch, heads, seq, dim, causal, steps, warmup, re
     return wall_ms, per_kernel
 
 
-def bench_gemm(core, ops, n, steps, warmup, repeats):
+def bench_gemm(core, ops, n, warmup, sample_ms):
     from triton_metal.buffer import DeviceBuffer
     a = DeviceBuffer((n, n), "bfloat16").write(normal_bf16((n, n), 1))
     b = DeviceBuffer((n, n), "bfloat16").write(normal_bf16((n, n), 2))
@@ -159,7 +169,7 @@ def bench_gemm(core, ops, n, steps, warmup, repeats):
         for _ in range(warmup):
             core.launch_async(kernel, grid, 128, kinds, values)
         core.synchronize()
-        ms = kernel_ms(core, kernel, grid, kinds, values, max(steps, repeats))
+        ms = kernel_ms(core, kernel, grid, kinds, values, sample_ms)
         variant = core.kernel_variant(kernel)
     finally:
         for x in (a, b, c):
@@ -257,7 +267,7 @@ def main():
     if args.only in ("all", "fa"):
         B, H, S, D = 4, 32, 4096, 128
         wall_ms, kernels = bench_attention(core, ops, B, H, S, D, True, args.steps, args.warmup,
-                                           args.kernel_repeats)
+                                           args.sample_ms)
         f_fwd = R.attention_flops(B * H, S, D, True)
         f_bwd = R.attention_flops(B * H, S, D, True, backward=True)
         fwd_ms = kernels["attn_fwd"]["ms"]
@@ -295,7 +305,7 @@ def main():
 
         # forward only, B8 H16 S1024 D64 non-causal.
         _, k4 = bench_attention(core, ops, 8, 16, 1024, 64, False, 0, args.warmup,
-                                args.kernel_repeats * 5, backward=False)
+                                args.sample_ms, backward=False)
         f4 = R.attention_flops(8 * 16, 1024, 64, False)
         ms4 = k4["attn_fwd"]["ms"]
         components["fa2_fwd_config4"] = {"tflops": round(f4 / (ms4 * 1e-3) / 1e12, 2),
@@ -303,7 +313,7 @@ def main():
                                          "ms": round(ms4, 4), "variant": k4["attn_fwd"]["variant"]}
     if args.only in ("all", "gemm"):
         n = 8192
-        ms, variant = bench_gemm(core, ops, n, args.steps, args.warmup, args.kernel_repeats)
+        ms, variant = bench_gemm(core, ops, n, args.warmup, args.sample_ms)
         tf = R.gemm_flops(n, n, n) / (ms * 1e-3) / 1e12
         components["gemm_bf16_8192"] = {"tflops": round(tf, 2),
                                         "frac_of_peak": round(tf / 2500, 4),

@@ -190,93 +190,105 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   wait_vmem();
   __syncthreads();
 
-  /* One key block: prefetch block j+1 into `nxt`, compute block j from `cur`. */
-  auto step = [&](const char *cur, char *nxt, int j) {
+  /* One key block: prefetch block j+1 into `nxt`, compute block j from `cur`.
+   * EDGE blocks (the causal diagonal band, a ragged end) apply the mask;
+   * interior blocks are straight-line code. */
+  auto step = [&](auto edge_tag, const char *cur, char *nxt, int j) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
     const int k0 = j * BN;
     if (j + 1 < nblocks) {
       stage_rows<T, D, BN>(Kg, ss, k0 + BN, n, nxt, wave, lane);
       stage_rows<T, D, BN>(Vg, ss, k0 + BN, n, nxt + TILE, wave, lane);
     }
-    const bool active = !CAUSAL || k0 <= qw0 + QW - 1;
-    if (active) {
-      /* S^T = K Q^T: 4 key tiles x 2 query tiles */
-      f32x4 s[4][2];
+    /* S^T = K Q^T: 4 key tiles x 2 query tiles */
+    f32x4 s[4][2];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        s[kt][0] = s[kt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int kt = 0; kt < 4; ++kt) {
+      s[kt][0] = s[kt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const v8 a = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D>(kt * 16 + c, ks * 4 + g)));
-          s[kt][0] = mfma_16x16x32(a, as_vec8<T>(qf[0][ks]), s[kt][0]);
-          s[kt][1] = mfma_16x16x32(a, as_vec8<T>(qf[1][ks]), s[kt][1]);
-        }
+      for (int ks = 0; ks < KS; ++ks) {
+        const v8 a = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D>(kt * 16 + c, ks * 4 + g)));
+        s[kt][0] = mfma_16x16x32(a, as_vec8<T>(qf[0][ks]), s[kt][0]);
+        s[kt][1] = mfma_16x16x32(a, as_vec8<T>(qf[1][ks]), s[kt][1]);
       }
-      const bool edge = (k0 + BN > n) || (CAUSAL && k0 + BN - 1 > qw0);
-      u32x4 pf[2][2]; /* P^T B operand: [query tile][key k-step] */
-      float alpha[2];
+    }
+    u32x4 pf[2][2]; /* P^T B operand: [query tile][key k-step] */
+    float alpha[2];
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < 2; ++qt) {
+      if (EDGE) {
         const int qi = qw0 + qt * 16 + c;
-        if (edge) {
-#pragma unroll
-          for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int key = k0 + kt * 16 + 4 * g + r;
-              if (key >= n || (CAUSAL && key > qi)) s[kt][qt][r] = TM_NEG_INF;
-            }
-        }
-        float mx = s[0][qt][0];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][qt][r]);
-        mx = group4_max(mx) * qk_scale;
-        const float m_new = fmaxf(m_i[qt], mx);
-        alpha[qt] = fast_exp2(m_i[qt] - m_new);
-        m_i[qt] = m_new;
-        float rs = 0.f;
-        float pv[4][4];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            pv[kt][r] = fast_exp2(__builtin_fmaf(s[kt][qt][r], qk_scale, -m_new));
-            rs += pv[kt][r];
+            const int key = k0 + kt * 16 + 4 * g + r;
+            s[kt][qt][r] = (key >= n || (CAUSAL && key > qi)) ? TM_NEG_INF : s[kt][qt][r];
           }
-        l_i[qt] = l_i[qt] * alpha[qt] + rs;
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          pf[qt][kk][0] = pack2<T>(pv[2 * kk][0], pv[2 * kk][1]);
-          pf[qt][kk][1] = pack2<T>(pv[2 * kk][2], pv[2 * kk][3]);
-          pf[qt][kk][2] = pack2<T>(pv[2 * kk + 1][0], pv[2 * kk + 1][1]);
-          pf[qt][kk][3] = pack2<T>(pv[2 * kk + 1][2], pv[2 * kk + 1][3]);
-        }
       }
+      float mx = s[0][qt][0];
 #pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) {
-        acc[dt][0] *= alpha[0];
-        acc[dt][1] *= alpha[1];
-      }
-      /* O^T += V^T P^T */
-      const char *vt = cur + TILE;
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) {
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][qt][r]);
+      mx = group4_max(mx) * qk_scale;
+      /* a row whose keys are all masked so far keeps m = -inf: use 0 as the
+       * offset so exp2 sees -inf - 0, not -inf - -inf */
+      const float m_new = fmaxf(m_i[qt], mx);
+      const float m_use = m_new == TM_NEG_INF ? 0.f : m_new;
+      alpha[qt] = fast_exp2(m_i[qt] - m_use);
+      m_i[qt] = m_new;
+      float rs = 0.f;
+      float pv[4][4];
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const v8 a = as_vec8<T>(read_kmajor_operand<D>(vt, 32 * kk, dt * 16, g, c));
-          acc[dt][0] = mfma_16x16x32(a, as_vec8<T>(pf[0][kk]), acc[dt][0]);
-          acc[dt][1] = mfma_16x16x32(a, as_vec8<T>(pf[1][kk]), acc[dt][1]);
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pv[kt][r] = fast_exp2(__builtin_fmaf(s[kt][qt][r], qk_scale, -m_use));
+          rs += pv[kt][r];
         }
+      l_i[qt] = l_i[qt] * alpha[qt] + rs;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        pf[qt][kk][0] = pack2<T>(pv[2 * kk][0], pv[2 * kk][1]);
+        pf[qt][kk][1] = pack2<T>(pv[2 * kk][2], pv[2 * kk][3]);
+        pf[qt][kk][2] = pack2<T>(pv[2 * kk + 1][0], pv[2 * kk + 1][1]);
+        pf[qt][kk][3] = pack2<T>(pv[2 * kk + 1][2], pv[2 * kk + 1][3]);
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+      acc[dt][0] *= alpha[0];
+      acc[dt][1] *= alpha[1];
+    }
+    /* O^T += V^T P^T */
+    const char *vt = cur + TILE;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const v8 a = as_vec8<T>(read_kmajor_operand<D>(vt, 32 * kk, dt * 16, g, c));
+        acc[dt][0] = mfma_16x16x32(a, as_vec8<T>(pf[0][kk]), acc[dt][0]);
+        acc[dt][1] = mfma_16x16x32(a, as_vec8<T>(pf[1][kk]), acc[dt][1]);
       }
     }
     wait_vmem();
     __syncthreads();
   };
+  using Interior = std::integral_constant<bool, false>;
+  using Edge = std::integral_constant<bool, true>;
 
-  for (int j = 0; j < nblocks; j += 2) {
-    step(lds_a, lds_b, j);
-    if (j + 1 < nblocks) step(lds_b, lds_a, j + 1);
+  /* interior blocks (below every query of the workgroup, inside n) in pairs,
+   * then the masked rest */
+  const int n_interior = CAUSAL ? min(q0 / BN, n / BN) : n / BN;
+  int j = 0;
+  for (; j + 1 < n_interior; j += 2) {
+    step(Interior{}, lds_a, lds_b, j);
+    step(Interior{}, lds_b, lds_a, j + 1);
+  }
+  for (; j < nblocks; ++j) {
+    if ((j & 1) == 0) step(Edge{}, lds_a, lds_b, j);
+    else step(Edge{}, lds_b, lds_a, j);
   }
 
   /* epilogue: O = acc / l, L = m + log2(l) */
@@ -364,72 +376,77 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
   wait_vmem();
   __syncthreads();
 
-  auto step = [&](const char *cur, char *nxt, int j) {
+  auto step = [&](auto edge_tag, const char *cur, char *nxt, int j) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
     const int k0 = j * BN;
     if (j + 1 < nblocks) {
       stage_rows<T, D, BN>(Kg, ss, k0 + BN, n, nxt, wave, lane);
       stage_rows<T, D, BN>(Vg, ss, k0 + BN, n, nxt + TILE, wave, lane);
     }
-    const bool active = !CAUSAL || k0 <= qw0 + QW - 1;
-    if (active) {
-      f32x4 s[4][2], dp[4][2];
+    /* two 32-key halves: scores, dS, then the dQ MFMAs of that half, so only
+     * half of S^T and dP^T is live at a time */
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        s[kt][0] = s[kt][1] = dp[kt][0] = dp[kt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int kk = 0; kk < 2; ++kk) {
+      f32x4 s[2][2], dp[2][2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int kt = 2 * kk + h;
+        s[h][0] = s[h][1] = dp[h][0] = dp[h][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           const v8 ka = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D>(kt * 16 + c, ks * 4 + g)));
           const v8 va =
               as_vec8<T>(*(const u32x4 *)(cur + TILE + tile_off<D>(kt * 16 + c, ks * 4 + g)));
-          s[kt][0] = mfma_16x16x32(ka, as_vec8<T>(qf[0][ks]), s[kt][0]);
-          s[kt][1] = mfma_16x16x32(ka, as_vec8<T>(qf[1][ks]), s[kt][1]);
-          dp[kt][0] = mfma_16x16x32(va, as_vec8<T>(df[0][ks]), dp[kt][0]);
-          dp[kt][1] = mfma_16x16x32(va, as_vec8<T>(df[1][ks]), dp[kt][1]);
+          s[h][0] = mfma_16x16x32(ka, as_vec8<T>(qf[0][ks]), s[h][0]);
+          s[h][1] = mfma_16x16x32(ka, as_vec8<T>(qf[1][ks]), s[h][1]);
+          dp[h][0] = mfma_16x16x32(va, as_vec8<T>(df[0][ks]), dp[h][0]);
+          dp[h][1] = mfma_16x16x32(va, as_vec8<T>(df[1][ks]), dp[h][1]);
         }
       }
-      const bool edge = (k0 + BN > n) || (CAUSAL && k0 + BN - 1 > qw0);
-      u32x4 dsf[2][2];
+      u32x4 dsf[2];
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
         const int qi = qw0 + qt * 16 + c;
-        float ds[4][4];
+        float ds[2][4];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            float x = __builtin_fmaf(s[kt][qt][r], qk_scale, -lse[qt]);
-            if (edge) {
-              const int key = k0 + kt * 16 + 4 * g + r;
-              if (key >= n || (CAUSAL && key > qi)) x = TM_NEG_INF;
+            float x = __builtin_fmaf(s[h][qt][r], qk_scale, -lse[qt]);
+            if (EDGE) {
+              const int key = k0 + (2 * kk + h) * 16 + 4 * g + r;
+              x = (key >= n || (CAUSAL && key > qi)) ? TM_NEG_INF : x;
             }
-            ds[kt][r] = fast_exp2(x) * (dp[kt][qt][r] - dlt[qt]);
+            ds[h][r] = fast_exp2(x) * (dp[h][qt][r] - dlt[qt]);
           }
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          dsf[qt][kk][0] = pack2<T>(ds[2 * kk][0], ds[2 * kk][1]);
-          dsf[qt][kk][1] = pack2<T>(ds[2 * kk][2], ds[2 * kk][3]);
-          dsf[qt][kk][2] = pack2<T>(ds[2 * kk + 1][0], ds[2 * kk + 1][1]);
-          dsf[qt][kk][3] = pack2<T>(ds[2 * kk + 1][2], ds[2 * kk + 1][3]);
-        }
+        dsf[qt] = (u32x4){pack2<T>(ds[0][0], ds[0][1]), pack2<T>(ds[0][2], ds[0][3]),
+                          pack2<T>(ds[1][0], ds[1][1]), pack2<T>(ds[1][2], ds[1][3])};
       }
-      /* dQ^T += K^T dS^T */
+      /* dQ^T += K^T dS^T over this half's 32 keys */
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) {
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const v8 a = as_vec8<T>(read_kmajor_operand<D>(cur, 32 * kk, dt * 16, g, c));
-          acc[dt][0] = mfma_16x16x32(a, as_vec8<T>(dsf[0][kk]), acc[dt][0]);
-          acc[dt][1] = mfma_16x16x32(a, as_vec8<T>(dsf[1][kk]), acc[dt][1]);
-        }
+        const v8 a = as_vec8<T>(read_kmajor_operand<D>(cur, 32 * kk, dt * 16, g, c));
+        acc[dt][0] = mfma_16x16x32(a, as_vec8<T>(dsf[0]), acc[dt][0]);
+        acc[dt][1] = mfma_16x16x32(a, as_vec8<T>(dsf[1]), acc[dt][1]);
       }
+      /* keep the next half's loads below this point (register pressure) */
+      __builtin_amdgcn_sched_barrier(0);
     }
     wait_vmem();
     __syncthreads();
   };
+  using Interior = std::integral_constant<bool, false>;
+  using Edge = std::integral_constant<bool, true>;
 
-  for (int j = 0; j < nblocks; j += 2) {
-    step(lds_a, lds_b, j);
-    if (j + 1 < nblocks) step(lds_b, lds_a, j + 1);
+  const int n_interior = CAUSAL ? min(q0 / BN, n / BN) : n / BN;
+  int j = 0;
+  for (; j + 1 < n_interior; j += 2) {
+    step(Interior{}, lds_a, lds_b, j);
+    step(Interior{}, lds_b, lds_a, j + 1);
+  }
+  for (; j < nblocks; ++j) {
+    if ((j & 1) == 0) step(Edge{}, lds_a, lds_b, j);
+    else step(Edge{}, lds_b, lds_a, j);
   }
 
 #pragma unroll
@@ -512,90 +529,108 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
   wait_vmem();
   __syncthreads();
 
-  auto step = [&](const char *cur, char *nxt, int i) {
+  /* One query block: prefetch block i+1 into `nxt`, accumulate block i from
+   * `cur`.  EDGE blocks (the diagonal band, a ragged end) apply the mask and
+   * load L/Delta element-wise; interior blocks run straight-line code, so the
+   * dK/dV accumulators never cross a control-flow merge inside the loop. */
+  auto step = [&](auto edge_tag, const char *cur, char *nxt, int i) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
     const int qs = q_start + i * BM;
     if (i + 1 < nblocks) {
       stage_rows<T, D, BM>(Qg, ss, qs + BM, n, nxt, wave, lane);
       stage_rows<T, D, BM>(dOg, ss, qs + BM, n, nxt + TILE, wave, lane);
     }
-    const bool active = !CAUSAL || qs + BM - 1 >= kw0;
-    if (active) {
-      /* L and Delta of queries qs + qt*16 + 4g + {0..3} */
-      f32x4 lse[2], dlt[2];
-      if (qs + BM <= n) {
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-          lse[qt] = *(const f32x4 *)(Lg + qs + qt * 16 + 4 * g);
-          dlt[qt] = *(const f32x4 *)(Dg + qs + qt * 16 + 4 * g);
-        }
-      } else {
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int qi = min(qs + qt * 16 + 4 * g + r, n - 1);
-            lse[qt][r] = Lg[qi];
-            dlt[qt][r] = Dg[qi];
-          }
-      }
-      f32x4 s[2][2], dp[2][2];
+    /* L and Delta of queries qs + qt*16 + 4g + {0..3} */
+    f32x4 lse[2], dlt[2];
+    if (!EDGE) {
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
-        s[0][qt] = s[1][qt] = dp[0][qt] = dp[1][qt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        lse[qt] = *(const f32x4 *)(Lg + qs + qt * 16 + 4 * g);
+        dlt[qt] = *(const f32x4 *)(Dg + qs + qt * 16 + 4 * g);
+      }
+    } else {
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const v8 qa = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D>(qt * 16 + c, ks * 4 + g)));
-          const v8 da =
-              as_vec8<T>(*(const u32x4 *)(cur + TILE + tile_off<D>(qt * 16 + c, ks * 4 + g)));
+      for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-          for (int kt = 0; kt < 2; ++kt) {
-            s[kt][qt] = mfma_16x16x32(qa, as_vec8<T>(kf[kt][ks]), s[kt][qt]);
-            dp[kt][qt] = mfma_16x16x32(da, as_vec8<T>(vf[kt][ks]), dp[kt][qt]);
-          }
+        for (int r = 0; r < 4; ++r) {
+          const int qi = min(qs + qt * 16 + 4 * g + r, n - 1);
+          lse[qt][r] = Lg[qi];
+          dlt[qt][r] = Dg[qi];
         }
-      }
-      const bool edge = (qs + BM > n) || (CAUSAL && qs < kw0 + KW - 1);
-      u32x4 pf[2], dsf[2];
+    }
+    f32x4 s[2][2], dp[2][2];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const int key = kw0 + kt * 16 + c;
-        float pr[2][4], ds[2][4];
+    for (int qt = 0; qt < 2; ++qt) {
+      s[0][qt] = s[1][qt] = dp[0][qt] = dp[1][qt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float x = __builtin_fmaf(s[kt][qt][r], qk_scale, -lse[qt][r]);
-            if (edge) {
-              const int qi = qs + qt * 16 + 4 * g + r;
-              if (qi >= n || (CAUSAL && qi < key)) x = TM_NEG_INF;
-            }
-            pr[qt][r] = fast_exp2(x);
-            ds[qt][r] = pr[qt][r] * (dp[kt][qt][r] - dlt[qt][r]);
-          }
-        pf[kt] = (u32x4){pack2<T>(pr[0][0], pr[0][1]), pack2<T>(pr[0][2], pr[0][3]),
-                         pack2<T>(pr[1][0], pr[1][1]), pack2<T>(pr[1][2], pr[1][3])};
-        dsf[kt] = (u32x4){pack2<T>(ds[0][0], ds[0][1]), pack2<T>(ds[0][2], ds[0][3]),
-                          pack2<T>(ds[1][0], ds[1][1]), pack2<T>(ds[1][2], ds[1][3])};
-      }
-      /* dV^T += dO^T P, dK^T += Q^T dS */
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) {
-        const v8 doa = as_vec8<T>(read_kmajor_operand<D>(cur + TILE, 0, dt * 16, g, c));
-        const v8 qa = as_vec8<T>(read_kmajor_operand<D>(cur, 0, dt * 16, g, c));
+      for (int ks = 0; ks < KS; ++ks) {
+        const v8 qa = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D>(qt * 16 + c, ks * 4 + g)));
+        const v8 da =
+            as_vec8<T>(*(const u32x4 *)(cur + TILE + tile_off<D>(qt * 16 + c, ks * 4 + g)));
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-          dv[dt][kt] = mfma_16x16x32(doa, as_vec8<T>(pf[kt]), dv[dt][kt]);
-          dk[dt][kt] = mfma_16x16x32(qa, as_vec8<T>(dsf[kt]), dk[dt][kt]);
+          s[kt][qt] = mfma_16x16x32(qa, as_vec8<T>(kf[kt][ks]), s[kt][qt]);
+          dp[kt][qt] = mfma_16x16x32(da, as_vec8<T>(vf[kt][ks]), dp[kt][qt]);
         }
+      }
+    }
+    u32x4 pf[2], dsf[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int key = kw0 + kt * 16 + c;
+      float pr[2][4], ds[2][4];
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float x = __builtin_fmaf(s[kt][qt][r], qk_scale, -lse[qt][r]);
+          if (EDGE) {
+            const int qi = qs + qt * 16 + 4 * g + r;
+            x = (qi >= n || (CAUSAL && qi < key)) ? TM_NEG_INF : x;
+          }
+          pr[qt][r] = fast_exp2(x);
+          ds[qt][r] = pr[qt][r] * (dp[kt][qt][r] - dlt[qt][r]);
+        }
+      pf[kt] = (u32x4){pack2<T>(pr[0][0], pr[0][1]), pack2<T>(pr[0][2], pr[0][3]),
+                       pack2<T>(pr[1][0], pr[1][1]), pack2<T>(pr[1][2], pr[1][3])};
+      dsf[kt] = (u32x4){pack2<T>(ds[0][0], ds[0][1]), pack2<T>(ds[0][2], ds[0][3]),
+                        pack2<T>(ds[1][0], ds[1][1]), pack2<T>(ds[1][2], ds[1][3])};
+    }
+    /* dV^T += dO^T P, dK^T += Q^T dS */
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+      const v8 doa = as_vec8<T>(read_kmajor_operand<D>(cur + TILE, 0, dt * 16, g, c));
+      const v8 qa = as_vec8<T>(read_kmajor_operand<D>(cur, 0, dt * 16, g, c));
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        dv[dt][kt] = mfma_16x16x32(doa, as_vec8<T>(pf[kt]), dv[dt][kt]);
+        dk[dt][kt] = mfma_16x16x32(qa, as_vec8<T>(dsf[kt]), dk[dt][kt]);
       }
     }
     wait_vmem();
     __syncthreads();
   };
+  using Interior = std::integral_constant<bool, false>;
+  using Edge = std::integral_constant<bool, true>;
 
-  for (int i = 0; i < nblocks; i += 2) {
-    step(lds_a, lds_b, i);
-    if (i + 1 < nblocks) step(lds_b, lds_a, i + 1);
+  /* masked front: blocks below the workgroup's last key (rounded up to an even
+   * count so the interior pairs keep the buffer parity); interior pairs; a
+   * masked tail for a ragged end */
+  int front = CAUSAL ? (BN + BM - 1) / BM : 0;
+  front = min((front + 1) & ~1, nblocks);
+  const int full = (n - q_start) / BM; /* blocks entirely inside n */
+  int i = 0;
+  for (; i < front; i += 2) {
+    step(Edge{}, lds_a, lds_b, i);
+    if (i + 1 < nblocks) step(Edge{}, lds_b, lds_a, i + 1);
+  }
+  for (; i + 1 < full; i += 2) {
+    step(Interior{}, lds_a, lds_b, i);
+    step(Interior{}, lds_b, lds_a, i + 1);
+  }
+  for (; i < nblocks; ++i) {
+    if ((i & 1) == 0) step(Edge{}, lds_a, lds_b, i);
+    else step(Edge{}, lds_b, lds_a, i);
   }
 
 #pragma unroll
