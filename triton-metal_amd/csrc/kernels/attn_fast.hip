@@ -134,6 +134,9 @@ TM_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 /* ---- forward ------------------------------------------------------------- */
 
+/* Lazy-rescale threshold in log2 units (P <= 2^8 between rescales). */
+#define TM_RESCALE_THRESHOLD 8.0f
+
 template <typename T, int D, bool CAUSAL>
 TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   constexpr int BM = 128, BN = 64, QW = 32;
@@ -213,7 +216,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
       }
     }
     u32x4 pf[2][2]; /* P^T B operand: [query tile][key k-step] */
-    float alpha[2];
+    float mxs[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       if (EDGE) {
@@ -231,23 +234,37 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][qt][r]);
-      mx = group4_max(mx) * qk_scale;
-      /* a row whose keys are all masked so far keeps m = -inf: use 0 as the
-       * offset so exp2 sees -inf - 0, not -inf - -inf */
-      const float m_new = fmaxf(m_i[qt], mx);
-      const float m_use = m_new == TM_NEG_INF ? 0.f : m_new;
-      alpha[qt] = fast_exp2(m_i[qt] - m_use);
-      m_i[qt] = m_new;
+      mxs[qt] = group4_max(mx) * qk_scale;
+    }
+    /* Lazy rescale: a row's exponent offset m only moves when the block max
+     * exceeds it by more than TM_RESCALE_THRESHOLD (P then stays below 2^8).
+     * The final O = acc / l and L = m + log2(l) use the same m, so this is the
+     * same softmax; the O rescale (64 multiplies) runs only when some lane of
+     * the wave needs it. */
+    if (__builtin_amdgcn_ballot_w64(mxs[0] > m_i[0] + TM_RESCALE_THRESHOLD ||
+                                    mxs[1] > m_i[1] + TM_RESCALE_THRESHOLD) != 0) {
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const float m_new = fmaxf(m_i[qt], mxs[qt]);
+        const float alpha = fast_exp2(m_i[qt] - m_new);
+        m_i[qt] = m_new;
+        l_i[qt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) acc[dt][qt] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
       float rs = 0.f;
       float pv[4][4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          pv[kt][r] = fast_exp2(__builtin_fmaf(s[kt][qt][r], qk_scale, -m_use));
+          pv[kt][r] = fast_exp2(__builtin_fmaf(s[kt][qt][r], qk_scale, -m_i[qt]));
           rs += pv[kt][r];
         }
-      l_i[qt] = l_i[qt] * alpha[qt] + rs;
+      l_i[qt] += rs;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         pf[qt][kk][0] = pack2<T>(pv[2 * kk][0], pv[2 * kk][1]);
@@ -255,11 +272,6 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
         pf[qt][kk][2] = pack2<T>(pv[2 * kk + 1][0], pv[2 * kk + 1][1]);
         pf[qt][kk][3] = pack2<T>(pv[2 * kk + 1][2], pv[2 * kk + 1][3]);
       }
-    }
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
-      acc[dt][0] *= alpha[0];
-      acc[dt][1] *= alpha[1];
     }
     /* O^T += V^T P^T */
     const char *vt = cur + TILE;

@@ -431,7 +431,7 @@ struct Plan {
   hipFunction_t function = nullptr;
   std::string variant;
   unsigned grid[3] = {1, 1, 1};
-  unsigned block = 1;
+  unsigned block = 0; /* must be set by the planner; 0 is refused at enqueue */
   std::vector<unsigned char> kernarg; /* packed bytes */
   bool empty = false;                 /* nothing to compute (a zero-sized problem) */
   bool by_value_struct = true;        /* built-in: one struct argument */
@@ -611,16 +611,16 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         return plan;
       }
       if (attn_fast_ok(spec, p.stride_head, p.stride_seq, p.sm_scale)) {
-        const char *tag = getenv("TRITON_METAL_FWD_TAG");
-        plan.variant = format("tm_attn_fwd_%s_%s_d%d%s", tag ? tag : "fast", el, spec.head_dim,
+        plan.variant = format("tm_attn_fwd_fast_%s_d%d%s", el, spec.head_dim,
                               spec.causal ? "_causal" : "");
         plan.grid[0] = (unsigned)(cdiv(p.n_ctx, 128) * heads);
+        plan.block = 256;
       } else {
         plan.variant = attn_symbol("fwd", spec);
         plan.grid[0] = (unsigned)cdiv(p.n_ctx, 64);
         plan.grid[1] = (unsigned)heads;
+        plan.block = 256;
       }
-      plan.block = 256;
       set_kernarg(plan, p);
       break;
     }
@@ -808,6 +808,10 @@ int64_t max_threads(Kernel &k) {
 
 void enqueue(const Plan &plan, hipStream_t stream) {
   if (plan.empty) return;
+  if (!plan.function || plan.block == 0 || plan.block > 1024 || !plan.grid[0] || !plan.grid[1] ||
+      !plan.grid[2])
+    throw TmError("internal error: dispatch of '" + plan.variant +
+                  "' was not fully planned (no function, workgroup size or grid)");
   if (plan.by_value_struct) {
     void *params[] = {(void *)plan.kernarg.data()};
     hip_check(hipModuleLaunchKernel(plan.function, plan.grid[0], plan.grid[1], plan.grid[2],
