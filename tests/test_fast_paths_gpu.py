@@ -1,0 +1,169 @@
+"""The specialised gfx950 kernels: which shapes take them, and parity at their
+edges (tiny and ragged sequence lengths, padded strides, non-square GEMMs).
+Every case is checked against the fp64 oracle; the variant each dispatch ran is
+read back through tm_kernel_variant."""
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import generators as G
+from oracle import reference as R
+from oracle import tolerance as T
+from triton_metal import _core, ops
+from triton_metal.buffer import DeviceBuffer, round_to
+
+pytestmark = pytest.mark.gpu
+
+DT = {"f32": "float32", "f16": "float16", "bf16": "bfloat16"}
+
+
+def _attention(heads, seq, dim, element, causal, stride_seq=None, stride_head=None, seed=0):
+    """Forward + backward through the ABI with optional padded strides; returns
+    (outputs dict, variants, inputs)."""
+    ss = stride_seq or dim
+    sh = stride_head or seq * ss
+    total = (heads - 1) * sh + (seq - 1) * ss + dim
+    rng = np.random.default_rng(seed)
+    dense = [round_to(rng.standard_normal((heads, seq, dim), dtype=np.float32), element)
+             for _ in range(4)]
+
+    def scatter(x):
+        flat = np.zeros(total, np.float32)
+        for h in range(heads):
+            for i in range(seq):
+                flat[h * sh + i * ss: h * sh + i * ss + dim] = x[h, i]
+        return flat
+
+    def gather(flat):
+        return np.stack([np.stack([flat[h * sh + i * ss: h * sh + i * ss + dim] for i in range(seq)])
+                         for h in range(heads)])
+
+    lib = ops.library(element, dim, causal)
+    dtype = DT[element]
+    bufs = {k: DeviceBuffer.from_numpy(scatter(x), dtype) for k, x in zip(("q", "k", "v", "do"), dense)}
+    for k in ("o", "dq", "dk", "dv"):
+        bufs[k] = DeviceBuffer.from_numpy(np.zeros(total, np.float32), dtype)
+    bufs["lse"] = DeviceBuffer((heads, seq), "float32")
+    bufs["delta"] = DeviceBuffer((heads, seq), "float32")
+    h = lambda k: bufs[k].tm_handle
+    scale = 1 / math.sqrt(dim)
+    B, I, F = _core.ARG_BUFFER, _core.ARG_I32, _core.ARG_F32
+    kern = lib.kernels
+    variants = []
+    try:
+        _core.launch(kern["attn_fwd"], (1, heads, 1), 128, [B, B, B, B, F, I, I, I, B, I],
+                     [h("q"), h("k"), h("v"), h("o"), _core.float_bits(scale), sh, ss, seq,
+                      h("lse"), seq])
+        variants.append(_core.kernel_variant(kern["attn_fwd"]))
+        _core.launch(kern["attn_bwd_preprocess"], (1, heads, 1), 128, [B, B, B, I, I, I, I],
+                     [h("o"), h("do"), h("delta"), sh, ss, seq, seq])
+        _core.launch(kern["attn_bwd_dq"], (1, heads, 1), 128, [B] * 7 + [F, I, I, I, I],
+                     [h(x) for x in ("q", "k", "v", "do", "dq", "lse", "delta")] +
+                     [_core.float_bits(scale), sh, ss, seq, seq])
+        variants.append(_core.kernel_variant(kern["attn_bwd_dq"]))
+        _core.launch(kern["attn_bwd_dkdv"], (1, heads, 1), 128, [B] * 8 + [F, I, I, I, I],
+                     [h(x) for x in ("q", "k", "v", "do", "dk", "dv", "lse", "delta")] +
+                     [_core.float_bits(scale), sh, ss, seq, seq])
+        variants.append(_core.kernel_variant(kern["attn_bwd_dkdv"]))
+        out = {k: gather(bufs[k].float32()) for k in ("o", "dq", "dk", "dv")}
+        out["lse"] = bufs["lse"].float32()
+        out["padding"] = [bufs[k].float32() for k in ("o", "dq", "dk", "dv")]
+    finally:
+        for b in bufs.values():
+            b.free()
+    return out, variants, dense, (total, sh, ss)
+
+
+def _check(out, dense, dim, causal, tol=2e-2):
+    q, k, v, d_out = dense
+    want = R.attention_backward(q, k, v, d_out, 1 / math.sqrt(dim), causal)
+    assert T.max_abs_error(out["o"], want["o"]) <= tol
+    assert T.max_abs_error(out["lse"], want["lse"]) <= 2e-3
+    for name in ("dq", "dk", "dv"):
+        assert T.hybrid_error(out[name], want[name]) <= tol, name
+
+
+@pytest.mark.parametrize("element", ["bf16", "f16"])
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("seq", [1, 2, 3, 63, 64, 65, 129])
+def test_fast_attention_edges(element, dim, causal, seq, device):
+    out, variants, dense, _ = _attention(2, seq, dim, element, causal)
+    assert all("_fast_" in v for v in variants), variants
+    _check(out, dense, dim, causal)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_fast_attention_padded_strides_leave_padding_untouched(causal, device):
+    """Rows padded to stride_seq = D + 8 and heads to a padded stride_head: the
+    fast kernels run (16-byte aligned rows) and never write the padding."""
+    heads, seq, dim = 3, 100, 64
+    out, variants, dense, (total, sh, ss) = _attention(heads, seq, dim, "bf16", causal,
+                                                        stride_seq=dim + 8,
+                                                        stride_head=seq * (dim + 8) + 16)
+    assert all("_fast_" in v for v in variants), variants
+    _check(out, dense, dim, causal)
+    mask = np.ones(total, bool)
+    for h in range(heads):
+        for i in range(seq):
+            mask[h * sh + i * ss: h * sh + i * ss + dim] = False
+    for flat in out["padding"]:
+        assert np.all(flat[mask] == 0)
+
+
+@pytest.mark.parametrize("element,dim,stride_seq,expect", [
+    ("bf16", 80, 80, "generic"),    # head_dim without a specialised kernel
+    ("bf16", 64, 68, "generic"),    # rows not 16-byte aligned
+    ("f32", 64, 64, "generic"),     # f32 runs the exact-f32 MFMA kernels
+    ("f16", 128, 128, "fast"),
+    ("bf16", 64, 72, "fast"),      # padded rows, 16-byte aligned
+])
+def test_variant_selection(element, dim, stride_seq, expect, device):
+    out, variants, dense, _ = _attention(1, 70, dim, element, False, stride_seq=stride_seq)
+    assert all(f"_{expect}_" in v for v in variants), variants
+    _check(out, dense, dim, False, tol=2e-2 if element != "f32" else 1e-4)
+
+
+def _gemm(m, n, k, element, lda=None, ldb=None, ldc=None, seed=0):
+    lda, ldb, ldc = lda or k, ldb or n, ldc or n
+    rng = np.random.default_rng(seed)
+    a = round_to(rng.standard_normal((m, lda), dtype=np.float32), element)
+    b = round_to(rng.standard_normal((k, ldb), dtype=np.float32), element)
+    dtype = DT[element]
+    A = DeviceBuffer.from_numpy(a, dtype)
+    B = DeviceBuffer.from_numpy(b, dtype)
+    C = DeviceBuffer.from_numpy(np.full((m, ldc), -7.0, np.float32), dtype)
+    kern = ops.library(element).kernels["matmul_kernel"]
+    try:
+        grid, kinds, values = ops.matmul_args(A, B, C, m, n, k, (lda, 1, ldb, 1, ldc, 1))
+        _core.launch(kern, grid, 128, kinds, values)
+        variant = _core.kernel_variant(kern)
+        c = C.float32()
+    finally:
+        for x in (A, B, C):
+            x.free()
+    want = a[:, :k].astype(np.float64) @ b[:, :n].astype(np.float64)
+    return c, want, variant
+
+
+@pytest.mark.parametrize("element", ["bf16", "f16"])
+@pytest.mark.parametrize("m,n,k,lda,ldb,ldc", [
+    (256, 512, 64, None, None, None),
+    (512, 256, 192, None, None, None),
+    (768, 1024, 320, 328, 1032, 1040),   # padded leading dimensions, 16-byte aligned
+])
+def test_fast_gemm_shapes_and_strides(element, m, n, k, lda, ldb, ldc, device):
+    c, want, variant = _gemm(m, n, k, element, lda, ldb, ldc)
+    assert variant == f"tm_gemm_fast_{element}"
+    assert T.hybrid_error(c[:, :n], want) <= 2e-2
+    if ldc:
+        assert np.all(c[:, n:] == -7.0)
+
+
+@pytest.mark.parametrize("m,n,k", [(255, 256, 64), (256, 256, 60), (300, 200, 100)])
+def test_unaligned_gemm_takes_the_generic_kernel(m, n, k, device):
+    c, want, variant = _gemm(m, n, k, "bf16")
+    assert variant == "tm_gemm_generic_bf16"
+    assert T.hybrid_error(c, want) <= 2e-2

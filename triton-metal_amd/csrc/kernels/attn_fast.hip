@@ -514,6 +514,9 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
   T *dVg = (T *)p.dv + base;
   const float *Lg = p.lse + (int64_t)bh * p.stride_lse;
   const float *Dg = p.delta + (int64_t)bh * p.stride_lse;
+  /* interior blocks read L and Delta as float4 when this head's row is 16-byte
+   * aligned, element by element otherwise */
+  const bool lse_vec = ((bh * (int64_t)p.stride_lse) & 3) == 0;
 
   const int q_start = CAUSAL ? k0 : 0;
   const int nblocks = (n - q_start + BM - 1) / BM;
@@ -554,7 +557,7 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
     }
     /* L and Delta of queries qs + qt*16 + 4g + {0..3} */
     f32x4 lse[2], dlt[2];
-    if (!EDGE) {
+    if (!EDGE && lse_vec) {
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
         lse[qt] = *(const f32x4 *)(Lg + qs + qt * 16 + 4 * g);

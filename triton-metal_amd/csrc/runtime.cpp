@@ -683,7 +683,7 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         plan.empty = true;
         return plan;
       }
-      const bool fast = attn_fast_ok(spec, stride_head, stride_seq, sm_scale) && stride_lse % 4 == 0;
+      const bool fast = attn_fast_ok(spec, stride_head, stride_seq, sm_scale);
       if (fast) {
         plan.grid[0] = (unsigned)(cdiv(n_ctx, 128) * heads);
       } else {
