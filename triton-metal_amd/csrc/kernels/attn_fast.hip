@@ -486,7 +486,7 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
  * P and dS are rounded to the element type before their dots
  * (AttentionBackwardKernel.swift:357-369).  Causal: the heaviest key blocks
  * (lowest keys) run first and the query walk starts at the block's first key. */
-template <typename T, int D, bool CAUSAL>
+template <typename T, int D, bool CAUSAL, bool LSE_VEC>
 TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
   constexpr int BN = 128, KW = 32, BM = 32;
   constexpr int KS = D / 32;
@@ -514,9 +514,9 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
   T *dVg = (T *)p.dv + base;
   const float *Lg = p.lse + (int64_t)bh * p.stride_lse;
   const float *Dg = p.delta + (int64_t)bh * p.stride_lse;
-  /* interior blocks read L and Delta as float4 when this head's row is 16-byte
-   * aligned, element by element otherwise */
-  const bool lse_vec = ((bh * (int64_t)p.stride_lse) & 3) == 0;
+  /* LSE_VEC: stride_lse is a multiple of 4, so interior blocks read L and
+   * Delta as float4; otherwise element by element */
+  constexpr bool lse_vec = LSE_VEC;
 
   const int q_start = CAUSAL ? k0 : 0;
   const int nblocks = (n - q_start + BM - 1) / BM;
@@ -675,7 +675,11 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
    * not fit in 256 registers: one wave per SIMD, accumulators in AGPRs. */               \
   extern "C" __global__ __launch_bounds__(256) void tm_attn_dkdv_fast_##TN##_d##D##CN(        \
       TmAttnDkdvArgs p) {                                                                     \
-    attn_dkdv_fast<T, D, CAUSAL>(p);                                                          \
+    attn_dkdv_fast<T, D, CAUSAL, true>(p);                                                    \
+  }                                                                                           \
+  extern "C" __global__ __launch_bounds__(256) void tm_attn_dkdv_fast_sl_##TN##_d##D##CN(     \
+      TmAttnDkdvArgs p) {                                                                     \
+    attn_dkdv_fast<T, D, CAUSAL, false>(p);                                                   \
   }
 #define TM_BWD_FAST_ALL(T, TN)           \
   TM_BWD_FAST(T, TN, 64, false, )        \
