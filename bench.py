@@ -11,12 +11,14 @@ AttentionBackwardBenchmark.swift:45-49), halved for the causal mask.
 
 Also measured in the same run and reported under "components":
   - bf16 GEMM 8192^3 (BASELINE config 3), 2*M*N*K FLOPs;
-  - bf16 FA2 forward at B8 H16 S1024 D64 non-causal.
+  - bf16 FA2 forward at B8 H16 S1024 D64 non-causal (BASELINE config 4);
+  - the fused bf16 SAE encoder relu(x @ W_enc + b_enc) at 8192 x 2048 x 16384.
 Per-kernel durations come from HIP events recorded on the library's stream
 around back-to-back dispatches (tm_launch_timed).
 
-The CPU baseline times the repo's numpy restatement of the same attention maths
-(oracle/reference.py) on a bounded sample of the workload on the host cores.
+The CPU baseline times a numpy port of the reference's attention forward and
+backward (attention_training.py:170-187, causal) on a bounded sample of the
+workload on the host cores.
 Prints ONE JSON line.
 """
 
@@ -177,11 +179,46 @@ def bench_gemm(core, ops, n, warmup, sample_ms):
     return ms, variant
 
 
+def attention_flops(batch_heads, seq, dim, causal, backward=False) -> float:
+    """The reference's FLOP convention: 4*S^2*D forward, 10*S^2*D backward per
+    (batch*head) (AttentionBenchmark.swift:64-68, AttentionBackwardBenchmark.swift:45-49);
+    causal counts half (this build's convention)."""
+    per = (10.0 if backward else 4.0) * seq * seq * dim * batch_heads
+    return per / 2 if causal else per
+
+
+def gemm_flops(m, n, k) -> float:
+    """2*M*N*K (GEMMBenchmark.swift:449-451)."""
+    return 2.0 * m * n * k
+
+
+def bench_sae(core, ops, rows, model, features, warmup, sample_ms):
+    """The fused encoder relu(x @ W_enc + b_enc) in bf16 (sae_encode_kernel)."""
+    from triton_metal.buffer import DeviceBuffer
+    x = DeviceBuffer((rows, model), "bfloat16").write(normal_bf16((rows, model), 3))
+    w = DeviceBuffer((model, features), "bfloat16").write(normal_bf16((model, features), 4))
+    b = DeviceBuffer((features,), "bfloat16").write(normal_bf16((features,), 5))
+    out = DeviceBuffer((rows, features), "bfloat16")
+    try:
+        enc = ops.SAEEncoder("bf16")
+        grid, kinds, values = enc.args(x, w, b, out, rows, model, features)
+        for _ in range(warmup):
+            core.launch_async(enc.kernel, grid, 128, kinds, values)
+        core.synchronize()
+        ms = kernel_ms(core, enc.kernel, grid, kinds, values, sample_ms)
+        variant = core.kernel_variant(enc.kernel)
+    finally:
+        for a in (x, w, b, out):
+            a.free()
+    return ms, variant
+
+
 def cpu_baseline(target_seconds):
     """numpy (fp32 BLAS) causal attention forward + backward, one (batch, head)
     of config 5 at a time (S=4096, D=128), repeated until about
-    `target_seconds` of CPU work; GFLOP/s under the same FLOP convention."""
-    from oracle import reference as R  # the CPU restatement is the baseline only
+    `target_seconds` of CPU work; TFLOP/s under the same FLOP convention.  The
+    per-head body is the reference's numpy forward and backward
+    (python/examples/attention_training.py:170-187) with the causal mask."""
 
     seq, dim = 4096, 128
     scale = np.float32(1 / math.sqrt(dim))
@@ -212,8 +249,8 @@ def cpu_baseline(target_seconds):
         elapsed = time.perf_counter() - t0
         if elapsed >= target_seconds or heads >= 2048:
             break
-    flops = R.attention_flops(heads, seq, dim, True) + R.attention_flops(heads, seq, dim, True,
-                                                                         backward=True)
+    flops = attention_flops(heads, seq, dim, True) + attention_flops(heads, seq, dim, True,
+                                                                     backward=True)
     threads = os.cpu_count()
     try:
         from threadpoolctl import threadpool_info
@@ -252,7 +289,6 @@ def main():
               "shards over batch*heads with no communication).", file=sys.stderr)
         sys.exit(2)
 
-    from oracle import reference as R
     from triton_metal import _core as core
     from triton_metal import ops
 
@@ -268,8 +304,8 @@ def main():
         B, H, S, D = 4, 32, 4096, 128
         wall_ms, kernels = bench_attention(core, ops, B, H, S, D, True, args.steps, args.warmup,
                                            args.sample_ms)
-        f_fwd = R.attention_flops(B * H, S, D, True)
-        f_bwd = R.attention_flops(B * H, S, D, True, backward=True)
+        f_fwd = attention_flops(B * H, S, D, True)
+        f_bwd = attention_flops(B * H, S, D, True, backward=True)
         fwd_ms = kernels["attn_fwd"]["ms"]
         bwd_ms = sum(kernels[k]["ms"] for k in ("attn_bwd_preprocess", "attn_bwd_dq",
                                                  "attn_bwd_dkdv"))
@@ -306,7 +342,7 @@ def main():
         # forward only, B8 H16 S1024 D64 non-causal.
         _, k4 = bench_attention(core, ops, 8, 16, 1024, 64, False, 0, args.warmup,
                                 args.sample_ms, backward=False)
-        f4 = R.attention_flops(8 * 16, 1024, 64, False)
+        f4 = attention_flops(8 * 16, 1024, 64, False)
         ms4 = k4["attn_fwd"]["ms"]
         components["fa2_fwd_config4"] = {"tflops": round(f4 / (ms4 * 1e-3) / 1e12, 2),
                                          "frac_of_peak": round(f4 / (ms4 * 1e-3) / 1e12 / 2500, 4),
@@ -314,10 +350,18 @@ def main():
     if args.only in ("all", "gemm"):
         n = 8192
         ms, variant = bench_gemm(core, ops, n, args.warmup, args.sample_ms)
-        tf = R.gemm_flops(n, n, n) / (ms * 1e-3) / 1e12
+        tf = gemm_flops(n, n, n) / (ms * 1e-3) / 1e12
         components["gemm_bf16_8192"] = {"tflops": round(tf, 2),
                                         "frac_of_peak": round(tf / 2500, 4),
                                         "ms": round(ms, 4), "variant": variant}
+        # The fused SAE encoder at an 8x dictionary over 8192 tokens of width 2048.
+        rows, model, features = 8192, 2048, 16384
+        ms_s, variant_s = bench_sae(core, ops, rows, model, features, args.warmup,
+                                    args.sample_ms)
+        tf_s = gemm_flops(rows, features, model) / (ms_s * 1e-3) / 1e12
+        components["sae_encode_bf16_8192x2048x16384"] = {
+            "tflops": round(tf_s, 2), "frac_of_peak": round(tf_s / 2500, 4),
+            "ms": round(ms_s, 4), "variant": variant_s}
         if args.only == "gemm":
             result.update(value=round(tf, 3), ms_per_step=round(ms, 4),
                           roofline={"bound": "mfma", "kernel": variant, "achieved": round(tf, 2),

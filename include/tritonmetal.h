@@ -21,7 +21,8 @@
  *         [head_dim=N] [causal=0|1]" (tm_compile_msl), which names the
  *         library's hand-written gfx950 kernels for the dense hot path:
  *         matmul_kernel, attn_fwd, attn_bwd_preprocess, attn_bwd_dq,
- *         attn_bwd_dkdv, tm_probe.
+ *         attn_bwd_dkdv, sae_encode_kernel (relu(x @ W + b),
+ *         Sources/TritonMetalMLX/SAEEncoder.swift:29-40), tm_probe.
  *   - a "buffer" is device memory in HBM (hipMalloc).  tm_buffer_contents
  *     returns its device address (what a kernel sees); host access goes
  *     through tm_buffer_write / tm_buffer_read.

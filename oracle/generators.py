@@ -4,6 +4,8 @@ matrix()  Tests/TritonMetalCoreTests/DotTests.swift:32-34
 tensor()  Tests/TritonMetalCoreTests/AttentionTests.swift:56-62
           (same formula in AttentionBackwardTests.swift:199-204)
 ramp()    bench inputs (i % p)/p - 0.5, AttentionBenchmark.swift:354
+synthetic()  the SAE encoder's inputs, Tests/TritonMetalMLXTests/MLXTestSupport.swift:82-90
+          (same formula in Sources/tmsae/main.swift and python/examples/sae_encode.py:64-69)
 """
 
 import numpy as np
@@ -36,3 +38,13 @@ def normal(shape, seed: int, scale: float = 1.0) -> np.ndarray:
 
 def uniform(shape, seed: int, low=-1.0, high=1.0) -> np.ndarray:
     return np.random.default_rng(seed).uniform(low, high, size=shape).astype(np.float32)
+
+
+def synthetic(shape, offset: int = 0, modulus: int = 71) -> np.ndarray:
+    """Float(((i + offset) * 13) % modulus) / Float(modulus) - 0.5, each step in
+    float32 as the Swift expression evaluates it, reshaped to `shape`."""
+    shape = tuple(shape)
+    count = int(np.prod(shape)) if shape else 1
+    i = np.arange(count, dtype=np.int64)
+    bucket = (((i + offset) * 13) % modulus).astype(np.float32)
+    return (bucket / np.float32(modulus) - np.float32(0.5)).reshape(shape)

@@ -6,6 +6,8 @@ attention_forward    O, P, L (log2 units)               AttentionTests.swift:21-
                                                         AttentionKernel.swift:33-39 (L = m + log2 l)
 attention_backward   Delta, dQ, dK, dV, amplification   AttentionBackwardTests.swift:46-160;
                                                         attention_training.py:179-187
+sae_encode           relu(x @ W_enc + b_enc)            SAEEncoder.swift:1-20;
+                                                        sae_encode.py:60-61 (numpy reference)
 The causal mask (key j > query i excluded) is this build's extension; the
 reference has none.  Arrays are [heads, seq, dim].
 """
@@ -19,6 +21,11 @@ LOG2E = 1.4426950408889634
 
 def gemm(a, b) -> np.ndarray:
     return np.asarray(a, np.float64) @ np.asarray(b, np.float64)
+
+
+def sae_encode(x, w, b) -> np.ndarray:
+    """relu(x @ w + b) in fp64: the fused SAE encoder's definition."""
+    return np.maximum(gemm(x, w) + np.asarray(b, np.float64)[None, :], 0.0)
 
 
 def _scores(q, k, scale, causal):

@@ -139,7 +139,7 @@ def test_kernel_info_publishes_every_builtin(core):
     info = json.loads(core.kernel_info("builtin element=bf16 head_dim=128 causal=1"))
     kernels = {k["name"]: k for k in info["kernels"]}
     assert set(kernels) == {"matmul_kernel", "attn_fwd", "attn_bwd_preprocess", "attn_bwd_dq",
-                            "attn_bwd_dkdv", "tm_probe"}
+                            "attn_bwd_dkdv", "sae_encode_kernel", "tm_probe"}
     mm = kernels["matmul_kernel"]
     assert [a["dtype"] for a in mm["args"]] == ["bf16"] * 3 + ["i32"] * 9
     assert [a["kind"] for a in mm["args"]] == [0, 0, 0] + [1] * 9
@@ -155,11 +155,37 @@ def test_kernel_info_publishes_every_builtin(core):
         assert k["threads_per_threadgroup"] > 0 and k["block_size"] > 0
 
 
+def test_sae_encoder_declares_the_arguments_its_wrapper_binds(core):
+    # SAEEncoderTests.swift:138-145: four f32 pointers (x, w, b, out), three
+    # i32 scalars (M, D, F), block shape [64, 64].
+    info = json.loads(core.kernel_info("builtin element=f32"))
+    sae = {k["name"]: k for k in info["kernels"]}["sae_encode_kernel"]
+    assert [a["dtype"] for a in sae["args"]] == ["f32"] * 4 + ["i32"] * 3
+    assert [a["kind"] for a in sae["args"]] == [0] * 4 + [1] * 3
+    assert [a["index"] for a in sae["args"]] == list(range(7))
+    assert sae["block_shape"] == [64, 64]
+
+
+@pytest.mark.parametrize("shapes,message", [
+    # SAEEncoderTests.swift:118-135, same inputs and messages.
+    (((8, 64), (32, 128), (128,)), "contraction dimensions differ"),
+    (((8, 64), (64, 128), (64,)), "128 features but b_enc has 64"),
+    (((8,), (64, 128), (128,)), "expects x [M, D]"),
+    (((8, 64), (64, 128), (1, 128)), "expects x [M, D]"),
+])
+def test_sae_encoder_refuses_mismatched_shapes(shapes, message):
+    from triton_metal.ops import SAEEncoder
+    with pytest.raises(ValueError, match=re.escape(message)):
+        SAEEncoder.check_shapes(*shapes)
+    assert SAEEncoder.check_shapes((8, 64), (64, 128), (128,)) == (8, 64, 128)
+
+
 def test_builtin_kernels_load_by_reference_name(core):
     live = core.live_handle_count()
     lib = core.compile_msl("builtin element=f16 head_dim=80")
     handles = [core.load_kernel(lib, n) for n in
-               ("matmul_kernel", "attn_fwd", "attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv")]
+               ("matmul_kernel", "attn_fwd", "attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv",
+                "sae_encode_kernel")]
     assert all(h > 0 for h in handles)
     assert core.kernel_max_threads(handles[0]) >= 128
     with pytest.raises(RuntimeError, match=r"kernel 'add_kernel' not found in library \(available: "):

@@ -146,6 +146,35 @@ def test_generators_match_the_reference_formulas():
         set(np.arange(23.0)))
 
 
+def test_sae_generator_matches_hand_evaluated_values():
+    # MLXTestSupport.swift:82-90 with offset 1, modulus 71: 13/71 - 1/2, 26/71 - 1/2,
+    # ..., and at i = 5 the product 78 wraps to 7.
+    x = G.synthetic([2, 3], offset=1, modulus=71)
+    assert x.dtype == np.float32 and x.shape == (2, 3)
+    want = np.array([13, 26, 39, 52, 65, 7], np.float32) / np.float32(71) - np.float32(0.5)
+    assert np.array_equal(x.ravel(), want)
+    assert G.synthetic([1], offset=0)[0] == np.float32(-0.5)  # default modulus, i = 0
+    assert G.synthetic([3], offset=3, modulus=29)[2] == np.float32(65 % 29) / np.float32(29) - np.float32(0.5)
+
+
+def test_sae_oracle_against_brute_force_and_relu_properties():
+    # relu(x @ w + b) by explicit loops with exact summation, on a ragged shape.
+    x = G.synthetic([7, 13], offset=1)
+    w = G.synthetic([13, 5], offset=7, modulus=53)
+    b = G.synthetic([5], offset=3, modulus=29)
+    got = R.sae_encode(x, w, b)
+    for i in range(7):
+        for j in range(5):
+            pre = math.fsum(float(x[i, k]) * float(w[k, j]) for k in range(13)) + float(b[j])
+            assert got[i, j] == pytest.approx(max(pre, 0.0), abs=1e-15)
+    # A -5 bias drives every unit of this input to exactly zero
+    # (SAEEncoderTests.swift:70-82 uses the same bias).
+    assert np.count_nonzero(R.sae_encode(x, w, np.full(5, -5.0))) == 0
+    # With a zero-width contraction the output is relu(b) on every row.
+    z = R.sae_encode(np.zeros((3, 0)), np.zeros((0, 5)), b)
+    assert np.array_equal(z, np.tile(np.maximum(b.astype(np.float64), 0), (3, 1)))
+
+
 def test_tolerance_metrics():
     assert T.hybrid_error([1.0, 10.0], [1.0, 11.0]) == pytest.approx(1 / 11)
     assert T.hybrid_error([0.5], [0.0]) == pytest.approx(0.5)

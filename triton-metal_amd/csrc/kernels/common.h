@@ -7,6 +7,11 @@
  *   v_mfma_f32_16x16x4_f32    A: row l%16, k = g          B: col l%16, k = g
  *   v_mfma_f32_16x16x32_bf16  A: row l%16, k = 8g .. 8g+7 B: col l%16, k = 8g .. 8g+7
  *   (and _f16)                D: col l%16, rows 4g .. 4g+3 (4 floats)
+ *   v_mfma_f32_32x32x16_bf16  A: row l%32, k = 8h .. 8h+7 B: col l%32, k = 8h .. 8h+7
+ *   (and _f16, h = l / 32)    D: col l%32, rows 8j + 4h .. 8j + 4h + 3 in
+ *                                floats 4j .. 4j+3 (j = 0..3; 16 floats)
+ * On gfx950 the 32x32x16 form sustains close to the dense peak back to back;
+ * the 16x16x32 form issues at about four fifths of it.
  * The contraction index k may be permuted freely as long as A and B use the
  * same permutation; the attention kernels rely on that to feed the softmax
  * output (rows 4g..4g+3 of a 16-row tile) straight back in as a B operand.
@@ -58,6 +63,24 @@ TM_DEV f32x4 mfma_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
 }
 TM_DEV f32x4 mfma_16x16x32(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+TM_DEV f32x16 mfma_32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+TM_DEV f32x16 mfma_32x32x16(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+/* Epilogues of the GEMM kernels: the plain product (matmul_kernel) or
+ * relu(acc + bias[col]) on the fp32 accumulator before the single store
+ * (sae_encode_kernel, Sources/TritonMetalMLX/SAEEncoder.swift:1-20). */
+enum GemmEpilogue { EPI_NONE = 0, EPI_BIAS_RELU = 1 };
+
+template <typename T, int EPI>
+TM_DEV float gemm_epilogue(const TmGemmArgs &p, float acc, int col) {
+  if (EPI == EPI_BIAS_RELU) return fmaxf(acc + to_f32(((const T *)p.bias)[col]), 0.f);
+  return acc;
 }
 
 /* ---- wavefront reductions over the four 16-lane groups --------------------- */

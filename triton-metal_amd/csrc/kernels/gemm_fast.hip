@@ -104,7 +104,7 @@ TM_DEV uint32_t g_pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, t2));
 }
 
-template <typename T>
+template <typename T, int EPI>
 TM_DEV void gemm_fast(const TmGemmArgs &p) {
   typedef typename GVec8<T>::type v8;
   __shared__ __align__(1024) char lds_a0[A_TILE];
@@ -180,17 +180,24 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
     const int m = m0 + wm * 128 + i * 16 + c;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const int n = n0 + wn * 64 + j * 16 + 4 * g;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = gemm_epilogue<T, EPI>(p, acc[i][j][r], n + r);
       u32x2 w;
-      w[0] = g_pack2<T>(acc[i][j][0], acc[i][j][1]);
-      w[1] = g_pack2<T>(acc[i][j][2], acc[i][j][3]);
-      *(u32x2 *)(C + (int64_t)m * ldc + n0 + wn * 64 + j * 16 + 4 * g) = w;
+      w[0] = g_pack2<T>(v[0], v[1]);
+      w[1] = g_pack2<T>(v[2], v[3]);
+      *(u32x2 *)(C + (int64_t)m * ldc + n) = w;
     }
   }
 }
 
-extern "C" __global__ __launch_bounds__(512) void tm_gemm_fast_bf16(TmGemmArgs p) {
-  gemm_fast<bf16_t>(p);
-}
-extern "C" __global__ __launch_bounds__(512) void tm_gemm_fast_f16(TmGemmArgs p) {
-  gemm_fast<f16_t>(p);
-}
+#define TM_GEMM_FAST(T, TN)                                                                \
+  extern "C" __global__ __launch_bounds__(512) void tm_gemm_fast_##TN(TmGemmArgs p) {        \
+    gemm_fast<T, EPI_NONE>(p);                                                               \
+  }                                                                                          \
+  extern "C" __global__ __launch_bounds__(512) void tm_sae_fast_##TN(TmGemmArgs p) {         \
+    gemm_fast<T, EPI_BIAS_RELU>(p);                                                          \
+  }
+TM_GEMM_FAST(bf16_t, bf16)
+TM_GEMM_FAST(f16_t, f16)

@@ -21,7 +21,7 @@
  * the element type (GEMMKernel.swift:28-174; matmul.py:20-44).
  * 64x64 output tile per 256-thread workgroup, 4 waves in 2x2, 32x32 per wave.
  * ------------------------------------------------------------------------- */
-template <typename T>
+template <typename T, int EPI>
 TM_DEV void gemm_generic(const TmGemmArgs &p) {
   constexpr int BM = 64, BN = 64, BK = 16;
   __shared__ float As[BM][BK + 1];
@@ -78,7 +78,8 @@ TM_DEV void gemm_generic(const TmGemmArgs &p) {
         const int row = m0 + wm * 32 + i * 16 + 4 * g + r;
         const int col = n0 + wn * 32 + j * 16 + c;
         if (row < p.m && col < p.n)
-          C[(int64_t)row * p.scm + (int64_t)col * p.scn] = from_f32<T>(acc[i][j][r]);
+          C[(int64_t)row * p.scm + (int64_t)col * p.scn] =
+              from_f32<T>(gemm_epilogue<T, EPI>(p, acc[i][j][r], col));
       }
 }
 
@@ -438,11 +439,14 @@ extern "C" __global__ __launch_bounds__(64) void tm_probe(float *out) {
 
 /* ---- named instantiations (the symbols the runtime looks up) -------------- */
 
-#define TM_GEMM(T, NAME) \
-  extern "C" __global__ __launch_bounds__(256) void NAME(TmGemmArgs p) { gemm_generic<T>(p); }
-TM_GEMM(float, tm_gemm_generic_f32)
-TM_GEMM(f16_t, tm_gemm_generic_f16)
-TM_GEMM(bf16_t, tm_gemm_generic_bf16)
+#define TM_GEMM(T, NAME, SAE_NAME) \
+  extern "C" __global__ __launch_bounds__(256) void NAME(TmGemmArgs p) { gemm_generic<T, EPI_NONE>(p); } \
+  extern "C" __global__ __launch_bounds__(256) void SAE_NAME(TmGemmArgs p) {                 \
+    gemm_generic<T, EPI_BIAS_RELU>(p);                                                        \
+  }
+TM_GEMM(float, tm_gemm_generic_f32, tm_sae_generic_f32)
+TM_GEMM(f16_t, tm_gemm_generic_f16, tm_sae_generic_f16)
+TM_GEMM(bf16_t, tm_gemm_generic_bf16, tm_sae_generic_bf16)
 
 #define TM_PRE(T, NAME) \
   extern "C" __global__ __launch_bounds__(256) void NAME(TmAttnPreArgs p) { attn_pre_generic<T>(p); }

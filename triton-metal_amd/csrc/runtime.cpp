@@ -13,7 +13,8 @@
  *   launch   = hipModuleLaunchKernel on one library-owned stream
  *
  * Built-in kernels carry the reference's names and argument lists
- * (matmul_kernel, attn_fwd, attn_bwd_preprocess, attn_bwd_dq, attn_bwd_dkdv).
+ * (matmul_kernel, attn_fwd, attn_bwd_preprocess, attn_bwd_dq, attn_bwd_dkdv, and
+ * the fused SAE encoder sae_encode_kernel).
  * Their planner checks every argument on the host (kinds, signs, buffer
  * extents), picks the device function for the shape and fills a by-value
  * argument block (tm_args.h), so no malformed request reaches the GPU.
@@ -216,7 +217,7 @@ struct Library : Object {
   }
 };
 
-enum class Builtin { None, Matmul, AttnFwd, AttnPre, AttnDq, AttnDkdv, Probe };
+enum class Builtin { None, Matmul, AttnFwd, AttnPre, AttnDq, AttnDkdv, SaeEncode, Probe };
 
 struct Kernel : Object {
   Kind kind() const override { return Kind::Kernel; }
@@ -350,6 +351,8 @@ const std::vector<BuiltinInfo> &builtin_table() {
        {"E", "E", "E", "E", "E", "f32", "f32", "f32", "i32", "i32", "i32", "i32"}, 0},
       {Builtin::AttnDkdv, "attn_bwd_dkdv", {0, 0, 0, 0, 0, 0, 0, 0, 2, 1, 1, 1, 1},
        {"E", "E", "E", "E", "E", "E", "f32", "f32", "f32", "i32", "i32", "i32", "i32"}, 0},
+      {Builtin::SaeEncode, "sae_encode_kernel", {0, 0, 0, 0, 1, 1, 1},
+       {"E", "E", "E", "E", "i32", "i32", "i32"}, 0},
       {Builtin::Probe, "tm_probe", {0}, {"f32"}, 0},
   };
   return table;
@@ -383,6 +386,7 @@ Published published_shape(Builtin id) {
     case Builtin::AttnPre: return {256, {64}};
     case Builtin::AttnDq: return {256, {64}};
     case Builtin::AttnDkdv: return {256, {64}};
+    case Builtin::SaeEncode: return {256, {64, 64}}; /* SAEEncoder.swift Blocking() */
     case Builtin::Probe: return {64, {256}};
     default: return {256, {1}};
   }
@@ -517,6 +521,28 @@ void validate_attn_common(const char *name, int64_t heads, int32_t stride_head,
   if (heads > 65535) throw TmError(format("%s: %lld heads exceeds 65535", name, (long long)heads));
 }
 
+/* Kernel choice shared by matmul_kernel and sae_encode_kernel: the specialised
+ * kernel takes 16-bit elements, row-major operands with unit inner stride and
+ * 16-byte aligned rows, in whole 256 x 256 x 64 tiles; anything else runs the
+ * generic 64 x 64 kernel. */
+void choose_gemm(Plan &plan, const TmGemmArgs &p, const BuiltinSpec &spec, const char *family) {
+  const char *el = element_name(spec.element);
+  const bool fast = fast_paths_enabled() && spec.element != Element::F32 && p.sak == 1 &&
+                    p.sbn == 1 && p.scn == 1 && p.m % 256 == 0 && p.n % 256 == 0 &&
+                    p.k % 64 == 0 && p.k > 0 && p.sam % 8 == 0 && p.sbk % 8 == 0 &&
+                    p.scm % 8 == 0;
+  if (fast) {
+    plan.variant = format("tm_%s_fast_%s", family, el);
+    plan.grid[0] = (unsigned)((p.m / 256) * (p.n / 256));
+    plan.block = 512;
+  } else {
+    plan.variant = format("tm_%s_generic_%s", family, el);
+    plan.grid[0] = (unsigned)cdiv(p.m, 64);
+    plan.grid[1] = (unsigned)cdiv(p.n, 64);
+    plan.block = 256;
+  }
+}
+
 Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, int64_t gx,
                   int64_t gy, int64_t gz) {
   const BuiltinInfo &info = *find_builtin(k.name);
@@ -559,22 +585,41 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         plan.empty = true;
         return plan;
       }
-      /* The specialised kernel: 16-bit elements, row-major operands with unit
-       * inner stride and 16-byte aligned rows, 256 x 256 x 64 tiles. */
-      const bool fast = fast_paths_enabled() && spec.element != Element::F32 && p.sak == 1 &&
-                        p.sbn == 1 && p.scn == 1 && p.m % 256 == 0 && p.n % 256 == 0 &&
-                        p.k % 64 == 0 && p.k > 0 && p.sam % 8 == 0 && p.sbk % 8 == 0 &&
-                        p.scm % 8 == 0;
-      if (fast) {
-        plan.variant = format("tm_gemm_fast_%s", el);
-        plan.grid[0] = (unsigned)((p.m / 256) * (p.n / 256));
-        plan.block = 512;
-      } else {
-        plan.variant = format("tm_gemm_generic_%s", el);
-        plan.grid[0] = (unsigned)cdiv(p.m, 64);
-        plan.grid[1] = (unsigned)cdiv(p.n, 64);
-        plan.block = 256;
+      choose_gemm(plan, p, spec, "gemm");
+      set_kernarg(plan, p);
+      break;
+    }
+    case Builtin::SaeEncode: {
+      /* relu(x @ w + b) with x [M, D], w [D, F], b [F], out [M, F], all
+       * row-major contiguous (SAEEncoder.swift:29-40). */
+      const char *nm = info.name;
+      const int32_t M = as_i32(args[4]), D = as_i32(args[5]), F = as_i32(args[6]);
+      require_nonneg(M, nm, "M");
+      require_nonneg(D, nm, "D");
+      require_nonneg(F, nm, "F");
+      TmGemmArgs p{};
+      p.a = args[0].buffer->ptr;
+      p.b = args[1].buffer->ptr;
+      p.bias = args[2].buffer->ptr;
+      p.c = args[3].buffer->ptr;
+      p.m = M;
+      p.n = F;
+      p.k = D;
+      p.sam = D;
+      p.sak = 1;
+      p.sbk = F;
+      p.sbn = 1;
+      p.scm = F;
+      p.scn = 1;
+      require_extent(args[0], (int64_t)M * D, es, nm, 0, "x");
+      require_extent(args[1], (int64_t)D * F, es, nm, 1, "w");
+      require_extent(args[2], F, es, nm, 2, "b");
+      require_extent(args[3], (int64_t)M * F, es, nm, 3, "out");
+      if (M == 0 || F == 0) {
+        plan.empty = true;
+        return plan;
       }
+      choose_gemm(plan, p, spec, "sae");
       set_kernarg(plan, p);
       break;
     }

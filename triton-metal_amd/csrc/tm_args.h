@@ -24,6 +24,7 @@ struct TmGemmArgs {
   void *c;
   int32_t m, n, k;
   int32_t sam, sak, sbk, sbn, scm, scn;
+  const void *bias; /* [n] elements; read only by the bias + ReLU epilogue kernels */
 };
 
 struct TmAttnFwdArgs {

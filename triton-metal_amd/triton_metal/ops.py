@@ -5,7 +5,10 @@ These are the reference's own callers restated for the built-in gfx950 kernels:
     the 12-argument matmul_kernel list);
   - `AttentionLayer` follows python/examples/attention_training.py:195-247
     (forward writes O and the log2 logsumexp L; backward runs preprocess, dq,
-    dkdv with the reference's argument lists and grids).
+    dkdv with the reference's argument lists and grids);
+  - `SAEEncoder` follows Sources/TritonMetalMLX/SAEEncoder.swift:116-160 and
+    python/examples/sae_encode.py:73-107 (relu(x @ W_enc + b_enc) in one
+    dispatch of sae_encode_kernel, grid (cdiv(M,64), cdiv(F,64))).
 Every dispatch is a tm_launch (or tm_launch_async) call into the native library.
 """
 
@@ -30,7 +33,8 @@ def cdiv(a, b):
 class BuiltinLibrary:
     """One built-in library spec and its five kernels, loaded once."""
 
-    NAMES = ("matmul_kernel", "attn_fwd", "attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv")
+    NAMES = ("matmul_kernel", "attn_fwd", "attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv",
+             "sae_encode_kernel")
 
     def __init__(self, element="f32", head_dim=64, causal=False):
         if element not in _ELEMENTS:
@@ -108,6 +112,80 @@ def matmul_numpy(a: np.ndarray, b: np.ndarray, element="f32") -> np.ndarray:
     finally:
         for x in (*bufs, c):
             x.free()
+
+
+# --------------------------------------------------------------------------- #
+# SAE encoder: relu(x @ W_enc + b_enc)
+# --------------------------------------------------------------------------- #
+
+
+class SAEEncoder:
+    """The fused sparse-autoencoder encoder `relu(x @ W_enc + b_enc)`, x [M, D],
+    W_enc [D, F], b_enc [F], out [M, F], all row-major contiguous.
+
+    Compiled once (the library cache), each call is one sae_encode_kernel
+    dispatch, as SAEEncoder.Compiled (SAEEncoder.swift:116-160).  The shape
+    checks and their messages are the Swift wrapper's (:127-143); the kernel
+    itself checks buffer extents against M, D and F."""
+
+    #: SAEEncoder.Blocking() defaults; the grid below is the reference caller's
+    #: (sae_encode.py:36-37, :97-103).
+    BLOCK_M = 64
+    BLOCK_F = 64
+
+    def __init__(self, element="f32"):
+        self.element = element
+        self.lib = library(element)
+        self.kernel = self.lib.kernels["sae_encode_kernel"]
+
+    @classmethod
+    def args(cls, x, w, b, out, rows, model, features):
+        """(grid, kinds, values) in the kernel's argument order (x, w, b, out, M, D, F)."""
+        grid = (cdiv(rows, cls.BLOCK_M), cdiv(features, cls.BLOCK_F), 1)
+        kinds = [_core.ARG_BUFFER] * 4 + [_core.ARG_I32] * 3
+        values = [x.tm_handle, w.tm_handle, b.tm_handle, out.tm_handle, rows, model, features]
+        return grid, kinds, values
+
+    @staticmethod
+    def check_shapes(x_shape, w_shape, b_shape):
+        """(rows, model, features), or ValueError with the Swift wrapper's message."""
+        x_shape, w_shape, b_shape = tuple(x_shape), tuple(w_shape), tuple(b_shape)
+        if len(x_shape) != 2 or len(w_shape) != 2 or len(b_shape) != 1:
+            raise ValueError(f"sae_encode expects x [M, D], W_enc [D, F], b_enc [F]; got "
+                             f"{list(x_shape)}, {list(w_shape)}, {list(b_shape)}")
+        rows, model = x_shape
+        features = w_shape[1]
+        if w_shape[0] != model:
+            raise ValueError(f"x is [{rows}, {model}] and W_enc is {list(w_shape)}; their "
+                             "contraction dimensions differ")
+        if b_shape[0] != features:
+            raise ValueError(f"W_enc has {features} features but b_enc has {b_shape[0]}")
+        return rows, model, features
+
+    def __call__(self, x: DeviceBuffer, w: DeviceBuffer, b: DeviceBuffer,
+                 out: DeviceBuffer = None, synchronous=True) -> DeviceBuffer:
+        rows, model, features = self.check_shapes(x.shape, w.shape, b.shape)
+        if out is None:
+            out = DeviceBuffer((rows, features), x.dtype)
+        elif tuple(out.shape) != (rows, features):
+            raise ValueError(f"out is {list(out.shape)}, expected [{rows}, {features}]")
+        grid, kinds, values = self.args(x, w, b, out, rows, model, features)
+        _go(self.kernel, grid, kinds, values, synchronous)
+        return out
+
+    def numpy(self, x: np.ndarray, w: np.ndarray, b: np.ndarray) -> np.ndarray:
+        """Host arrays in, float32 host array out."""
+        self.check_shapes(np.shape(x), np.shape(w), np.shape(b))
+        dtype = _ELEMENTS[self.element]
+        bufs = [DeviceBuffer.from_numpy(np.asarray(a, np.float32), dtype) for a in (x, w, b)]
+        out = None
+        try:
+            out = self(*bufs)
+            return out.float32()
+        finally:
+            for a in (*bufs, out):
+                if a is not None:
+                    a.free()
 
 
 # --------------------------------------------------------------------------- #
