@@ -70,6 +70,18 @@ TM_DEV void global_to_lds16(const void *src, char *lds_wave_base) {
   __builtin_amdgcn_global_load_lds(src, (lds_void *)lds_wave_base, 16, 0, 0);
 }
 
+/* Per-row statistics of one block of 32 queries, HBM -> LDS with the tiles:
+ * wave 0 copies L[q0 .. q0+31] then Delta[q0 .. q0+31] (one 4-byte element per
+ * lane; rows past n repeat row n-1 and are masked by the caller), so the
+ * block's L and Delta arrive under the same wait as its Q and dO rows. */
+TM_DEV void stage_stats(const float *L, const float *Dl, int q0, int n, char *lds, int wave,
+                        int lane) {
+  if (wave != 0) return;
+  const int q = min(q0 + (lane & 31), n - 1);
+  const float *src = lane < 32 ? L + q : Dl + q;
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)lds, 4, 0, 0);
+}
+
 /* wait for this wave's outstanding vector-memory operations (vmcnt = 0) */
 TM_DEV void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -485,14 +497,25 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
  *   dV^T += dO^T P, dK^T += Q^T dS         (dO^T, Q^T: ds_read_b64_tr_b16)
  * P and dS are rounded to the element type before their dots
  * (AttentionBackwardKernel.swift:357-369).  Causal: the heaviest key blocks
- * (lowest keys) run first and the query walk starts at the block's first key. */
-template <typename T, int D, bool CAUSAL, bool LSE_VEC>
+ * (lowest keys) run first and the query walk starts at the block's first key.
+ *
+ * Software pipeline over query blocks, three LDS buffers in rotation: step i
+ * issues the copy of block i+2, computes S, dP, P and dS of block i+1, and
+ * accumulates dV, dK from block i's P and dS (kept in registers since step
+ * i-1).  The softmax of one block and the gradient MFMAs of the previous one
+ * are independent, so the wave's VALU work overlaps its MFMA work.  Buffer
+ * indices are compile-time (PH = i mod 3) so the compiler sees that the
+ * in-flight copy never aliases the tiles being read. */
+template <typename T, int D, bool CAUSAL>
 TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
   constexpr int BN = 128, KW = 32, BM = 32;
   constexpr int KS = D / 32;
   constexpr int TILE = BM * D * 2;
-  __shared__ __align__(1024) char lds_a[2 * TILE];
-  __shared__ __align__(1024) char lds_b[2 * TILE];
+  constexpr int STATS = 2 * TILE; /* L[32] then Delta[32], fp32 */
+  constexpr int BUF = 2 * TILE + 256;
+  __shared__ __align__(1024) char lds_0[BUF];
+  __shared__ __align__(1024) char lds_1[BUF];
+  __shared__ __align__(1024) char lds_2[BUF];
 
   typedef typename Vec8<T>::type v8;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -514,16 +537,16 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
   T *dVg = (T *)p.dv + base;
   const float *Lg = p.lse + (int64_t)bh * p.stride_lse;
   const float *Dg = p.delta + (int64_t)bh * p.stride_lse;
-  /* LSE_VEC: stride_lse is a multiple of 4, so interior blocks read L and
-   * Delta as float4; otherwise element by element */
-  constexpr bool lse_vec = LSE_VEC;
 
   const int q_start = CAUSAL ? k0 : 0;
   const int nblocks = (n - q_start + BM - 1) / BM;
-  if (nblocks > 0) {
-    stage_rows<T, D, BM>(Qg, ss, q_start, n, lds_a, wave, lane);
-    stage_rows<T, D, BM>(dOg, ss, q_start, n, lds_a + TILE, wave, lane);
-  }
+
+  auto stage = [&](char *buf, int blk) {
+    const int qs = q_start + blk * BM;
+    stage_rows<T, D, BM>(Qg, ss, qs, n, buf, wave, lane);
+    stage_rows<T, D, BM>(dOg, ss, qs, n, buf + TILE, wave, lane);
+    stage_stats(Lg, Dg, qs, n, buf + STATS, wave, lane);
+  };
 
   u32x4 kf[2][KS], vf[2][KS];
 #pragma unroll
@@ -541,37 +564,18 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
   for (int dt = 0; dt < D / 16; ++dt)
     dk[dt][0] = dk[dt][1] = dv[dt][0] = dv[dt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  wait_vmem();
-  __syncthreads();
-
-  /* One query block: prefetch block i+1 into `nxt`, accumulate block i from
-   * `cur`.  EDGE blocks (the diagonal band, a ragged end) apply the mask and
-   * load L/Delta element-wise; interior blocks run straight-line code, so the
-   * dK/dV accumulators never cross a control-flow merge inside the loop. */
-  auto step = [&](auto edge_tag, const char *cur, char *nxt, int i) {
+  /* S, dP, then P and dS (rounded, packed as MFMA B operands) of block `blk`
+   * from its tile.  EDGE blocks (the diagonal band, a ragged end) apply the
+   * mask; interior blocks run straight-line code. */
+  auto scores = [&](auto edge_tag, const char *cur, int blk, u32x4 (&pf)[2], u32x4 (&dsf)[2]) {
     constexpr bool EDGE = decltype(edge_tag)::value;
-    const int qs = q_start + i * BM;
-    if (i + 1 < nblocks) {
-      stage_rows<T, D, BM>(Qg, ss, qs + BM, n, nxt, wave, lane);
-      stage_rows<T, D, BM>(dOg, ss, qs + BM, n, nxt + TILE, wave, lane);
-    }
+    const int qs = q_start + blk * BM;
     /* L and Delta of queries qs + qt*16 + 4g + {0..3} */
     f32x4 lse[2], dlt[2];
-    if (!EDGE && lse_vec) {
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        lse[qt] = *(const f32x4 *)(Lg + qs + qt * 16 + 4 * g);
-        dlt[qt] = *(const f32x4 *)(Dg + qs + qt * 16 + 4 * g);
-      }
-    } else {
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int qi = min(qs + qt * 16 + 4 * g + r, n - 1);
-          lse[qt][r] = Lg[qi];
-          dlt[qt][r] = Dg[qi];
-        }
+    for (int qt = 0; qt < 2; ++qt) {
+      lse[qt] = *(const f32x4 *)(cur + STATS + (qt * 16 + 4 * g) * 4);
+      dlt[qt] = *(const f32x4 *)(cur + STATS + 128 + (qt * 16 + 4 * g) * 4);
     }
     f32x4 s[2][2], dp[2][2];
 #pragma unroll
@@ -589,7 +593,6 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
         }
       }
     }
-    u32x4 pf[2], dsf[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       const int key = kw0 + kt * 16 + c;
@@ -611,7 +614,10 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
       dsf[kt] = (u32x4){pack2<T>(ds[0][0], ds[0][1]), pack2<T>(ds[0][2], ds[0][3]),
                         pack2<T>(ds[1][0], ds[1][1]), pack2<T>(ds[1][2], ds[1][3])};
     }
-    /* dV^T += dO^T P, dK^T += Q^T dS */
+  };
+
+  /* dV^T += dO^T P, dK^T += Q^T dS for the block whose tile is `cur` */
+  auto grads = [&](const char *cur, const u32x4 (&pf)[2], const u32x4 (&dsf)[2]) {
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt) {
       const v8 doa = as_vec8<T>(read_kmajor_operand<D>(cur + TILE, 0, dt * 16, g, c));
@@ -622,30 +628,73 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
         dk[dt][kt] = mfma_16x16x32(qa, as_vec8<T>(dsf[kt]), dk[dt][kt]);
       }
     }
+  };
+
+  char *const bufs[3] = {lds_0, lds_1, lds_2};
+  u32x4 pf[2], dsf[2]; /* P and dS of the block whose gradients are pending */
+
+  /* Step i with buffer phase PH = i mod 3.  CHECKED steps test whether blocks
+   * i+1 and i+2 exist; unchecked (interior) steps know they do. */
+  auto step = [&](auto ph_tag, auto edge_tag, auto checked_tag, int i) {
+    constexpr int PH = decltype(ph_tag)::value;
+    constexpr bool CHECKED = decltype(checked_tag)::value;
+    char *cur = bufs[PH];
+    char *nx1 = bufs[(PH + 1) % 3];
+    char *nx2 = bufs[(PH + 2) % 3];
+    if (!CHECKED || i + 2 < nblocks) stage(nx2, i + 2);
+    u32x4 pf2[2], ds2[2];
+    if (!CHECKED || i + 1 < nblocks) scores(edge_tag, nx1, i + 1, pf2, ds2);
+    grads(cur, pf, dsf);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      pf[kt] = pf2[kt];
+      dsf[kt] = ds2[kt];
+    }
     wait_vmem();
     __syncthreads();
   };
   using Interior = std::integral_constant<bool, false>;
   using Edge = std::integral_constant<bool, true>;
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  using P2 = std::integral_constant<int, 2>;
+  auto checked_step = [&](auto edge_tag, int i) {
+    switch (i % 3) {
+      case 0: step(P0{}, edge_tag, Edge{}, i); break;
+      case 1: step(P1{}, edge_tag, Edge{}, i); break;
+      default: step(P2{}, edge_tag, Edge{}, i); break;
+    }
+  };
 
-  /* masked front: blocks below the workgroup's last key (rounded up to an even
-   * count so the interior pairs keep the buffer parity); interior pairs; a
-   * masked tail for a ragged end */
-  int front = CAUSAL ? (BN + BM - 1) / BM : 0;
-  front = min((front + 1) & ~1, nblocks);
-  const int full = (n - q_start) / BM; /* blocks entirely inside n */
+  if (nblocks > 0) {
+    stage(lds_0, 0);
+    if (nblocks > 1) stage(lds_1, 1);
+    wait_vmem();
+    __syncthreads();
+    scores(Edge{}, lds_0, 0, pf, dsf);
+  }
+
+  /* Block b is masked if it lies in the diagonal band (b < band) or runs past
+   * n (b >= full).  Step i masks the softmax of block i+1. */
+  const int band = CAUSAL ? (BN + BM - 1) / BM : 0;
+  const int full = (n - q_start) / BM;
   int i = 0;
-  for (; i < front; i += 2) {
-    step(Edge{}, lds_a, lds_b, i);
-    if (i + 1 < nblocks) step(Edge{}, lds_b, lds_a, i + 1);
+  /* front: steps whose next block is masked */
+  for (; i < nblocks && i + 1 < band; ++i) checked_step(Edge{}, i);
+  /* interior: next block unmasked, blocks i+1 and i+2 exist; peel to phase 0,
+   * then whole rotations */
+  const int interior_end = min(full - 1, nblocks - 2); /* last i with i+1 < full, i+2 < nblocks */
+  for (; i < interior_end && (i % 3) != 0; ++i) checked_step(Interior{}, i);
+  for (; i + 2 < interior_end; i += 3) {
+    step(P0{}, Interior{}, Interior{}, i);
+    step(P1{}, Interior{}, Interior{}, i + 1);
+    step(P2{}, Interior{}, Interior{}, i + 2);
   }
-  for (; i + 1 < full; i += 2) {
-    step(Interior{}, lds_a, lds_b, i);
-    step(Interior{}, lds_b, lds_a, i + 1);
-  }
+  for (; i < interior_end; ++i) checked_step(Interior{}, i);
+  /* tail: the rest, masked where needed */
   for (; i < nblocks; ++i) {
-    if ((i & 1) == 0) step(Edge{}, lds_a, lds_b, i);
-    else step(Edge{}, lds_b, lds_a, i);
+    if (i + 1 < full) checked_step(Interior{}, i);
+    else checked_step(Edge{}, i);
   }
 
 #pragma unroll
@@ -675,11 +724,7 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
    * not fit in 256 registers: one wave per SIMD, accumulators in AGPRs. */               \
   extern "C" __global__ __launch_bounds__(256) void tm_attn_dkdv_fast_##TN##_d##D##CN(        \
       TmAttnDkdvArgs p) {                                                                     \
-    attn_dkdv_fast<T, D, CAUSAL, true>(p);                                                    \
-  }                                                                                           \
-  extern "C" __global__ __launch_bounds__(256) void tm_attn_dkdv_fast_sl_##TN##_d##D##CN(     \
-      TmAttnDkdvArgs p) {                                                                     \
-    attn_dkdv_fast<T, D, CAUSAL, false>(p);                                                   \
+    attn_dkdv_fast<T, D, CAUSAL>(p);                                                          \
   }
 #define TM_BWD_FAST_ALL(T, TN)           \
   TM_BWD_FAST(T, TN, 64, false, )        \

@@ -735,12 +735,8 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         plan.grid[0] = (unsigned)cdiv(n_ctx, 64);
         plan.grid[1] = (unsigned)heads;
       }
-      /* dkdv reads L and Delta as float4 when stride_lse keeps rows 16-byte
-       * aligned; the _sl variant reads them element by element */
-      const std::string fast_name =
-          format("tm_attn_%s_fast_%s%s_d%d%s", dq ? "dq" : "dkdv",
-                 (!dq && stride_lse % 4 != 0) ? "sl_" : "", el, spec.head_dim,
-                 spec.causal ? "_causal" : "");
+      const std::string fast_name = format("tm_attn_%s_fast_%s_d%d%s", dq ? "dq" : "dkdv", el,
+                                           spec.head_dim, spec.causal ? "_causal" : "");
       plan.block = 256;
       if (dq) {
         TmAttnDqArgs p{};
