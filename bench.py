@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the baseline sample")
     ap.add_argument("--only", choices=["all", "fa", "gemm"], default="all")
+    ap.add_argument("--probes", action="store_true",
+                    help="print the device probe rates (MFMA shapes, exp2, LDS reads, fp32 atomics) "
+                         "as one JSON line and exit")
     ap.add_argument("--profile-pass", action="store_true",
                     help="for rocprofv3 --pmc runs: one copy kernel of known size (the "
                          "FETCH_SIZE / WRITE_SIZE calibration) and one dispatch of each hot kernel")
@@ -75,7 +78,7 @@ COPY_BYTES = 1 << 30
 def profile_pass(core, ops):
     """One copy of COPY_BYTES (reads and writes that many bytes of HBM), then one
     dispatch each of attn_fwd, attn_bwd_preprocess, attn_bwd_dq, attn_bwd_dkdv at
-    config 5 and matmul_kernel at config 3."""
+    config 5, matmul_kernel at config 3 and sae_encode_kernel at 8192 x 2048 x 16384."""
     from triton_metal.buffer import DeviceBuffer
     lib = core.compile_msl(COPY_SOURCE)
     kernel = core.load_kernel(lib, "tm_calibration_copy")
@@ -99,6 +102,13 @@ def profile_pass(core, ops):
     ops.matmul(a, b, c, n, n, n)
     for x in (a, b, c):
         x.free()
+    rows, model, features = 8192, 2048, 16384
+    x = DeviceBuffer((rows, model), "bfloat16").write(normal_bf16((rows, model), 3))
+    w = DeviceBuffer((model, features), "bfloat16").write(normal_bf16((model, features), 4))
+    bias = DeviceBuffer((features,), "bfloat16").write(normal_bf16((features,), 5))
+    out = ops.SAEEncoder("bf16")(x, w, bias)
+    for t in (x, w, bias, out):
+        t.free()
     print(json.dumps({"profile_pass": "done", "copy_bytes": COPY_BYTES}), flush=True)
 
 
@@ -294,6 +304,10 @@ def main():
 
     if not core.is_usable():
         raise SystemExit("no usable gfx950 device: " + str(core.unusable_reason()))
+    if args.probes:
+        from triton_metal import probes
+        print(json.dumps({"probes": probes.run(), "device": core.device_name()}))
+        return
     if args.profile_pass:
         profile_pass(core, ops)
         return
