@@ -77,12 +77,6 @@ TM_DEV f32x16 mfma_32x32x16(f16x8 a, f16x8 b, f32x16 c) {
  * (sae_encode_kernel, Sources/TritonMetalMLX/SAEEncoder.swift:1-20). */
 enum GemmEpilogue { EPI_NONE = 0, EPI_BIAS_RELU = 1 };
 
-template <typename T, int EPI>
-TM_DEV float gemm_epilogue(const TmGemmArgs &p, float acc, int col) {
-  if (EPI == EPI_BIAS_RELU) return fmaxf(acc + to_f32(((const T *)p.bias)[col]), 0.f);
-  return acc;
-}
-
 /* ---- wavefront reductions over the four 16-lane groups --------------------- */
 
 TM_DEV float group4_max(float x) {

@@ -175,6 +175,16 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
 
   /* acc[i][j] is the C^T tile: lane holds row m0 + wm*128 + i*16 + c,
    * columns n0 + wn*64 + j*16 + 4g .. +3 */
+  /* The bias of the wave's 16 columns, loaded once before any store (the
+   * compiler cannot move the loads across stores to C that might alias). */
+  float bias[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      bias[j][r] = EPI == EPI_BIAS_RELU
+                       ? to_f32(((const T *)p.bias)[n0 + wn * 64 + j * 16 + 4 * g + r])
+                       : 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int m = m0 + wm * 128 + i * 16 + c;
@@ -183,7 +193,8 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
       const int n = n0 + wn * 64 + j * 16 + 4 * g;
       float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = gemm_epilogue<T, EPI>(p, acc[i][j][r], n + r);
+      for (int r = 0; r < 4; ++r)
+        v[r] = EPI == EPI_BIAS_RELU ? fmaxf(acc[i][j][r] + bias[j][r], 0.f) : acc[i][j][r];
       u32x2 w;
       w[0] = g_pack2<T>(v[0], v[1]);
       w[1] = g_pack2<T>(v[2], v[3]);

@@ -69,6 +69,13 @@ TM_DEV void gemm_generic(const TmGemmArgs &p) {
     __syncthreads();
   }
 
+  /* the bias of this lane's two columns, loaded before any store to C */
+  float bias[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = n0 + wn * 32 + j * 16 + c;
+    bias[j] = (EPI == EPI_BIAS_RELU && col < p.n) ? to_f32(((const T *)p.bias)[col]) : 0.f;
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -77,9 +84,8 @@ TM_DEV void gemm_generic(const TmGemmArgs &p) {
       for (int r = 0; r < 4; ++r) {
         const int row = m0 + wm * 32 + i * 16 + 4 * g + r;
         const int col = n0 + wn * 32 + j * 16 + c;
-        if (row < p.m && col < p.n)
-          C[(int64_t)row * p.scm + (int64_t)col * p.scn] =
-              from_f32<T>(gemm_epilogue<T, EPI>(p, acc[i][j][r], col));
+        const float v = EPI == EPI_BIAS_RELU ? fmaxf(acc[i][j][r] + bias[j], 0.f) : acc[i][j][r];
+        if (row < p.m && col < p.n) C[(int64_t)row * p.scm + (int64_t)col * p.scn] = from_f32<T>(v);
       }
 }
 
