@@ -59,6 +59,7 @@ def _attention(heads, seq, dim, element, causal, stride_seq=None, stride_head=No
         variants.append(_core.kernel_variant(kern["attn_fwd"]))
         _core.launch(kern["attn_bwd_preprocess"], (1, heads, 1), 128, [B, B, B, I, I, I, I],
                      [h("o"), h("do"), h("delta"), sh, ss, seq, seq])
+        variants.append(_core.kernel_variant(kern["attn_bwd_preprocess"]))
         _core.launch(kern["attn_bwd_dq"], (1, heads, 1), 128, [B] * 7 + [F, I, I, I, I],
                      [h(x) for x in ("q", "k", "v", "do", "dq", "lse", "delta")] +
                      [_core.float_bits(scale), sh, ss, seq, seq])
@@ -69,6 +70,7 @@ def _attention(heads, seq, dim, element, causal, stride_seq=None, stride_head=No
         variants.append(_core.kernel_variant(kern["attn_bwd_dkdv"]))
         out = {k: gather(bufs[k].float32()) for k in ("o", "dq", "dk", "dv")}
         out["lse"] = bufs["lse"].float32()
+        out["delta"] = bufs["delta"].float32()
         out["padding"] = [bufs[k].float32() for k in ("o", "dq", "dk", "dv")]
     finally:
         for b in bufs.values():
@@ -81,6 +83,12 @@ def _check(out, dense, dim, causal, tol=2e-2):
     want = R.attention_backward(q, k, v, d_out, 1 / math.sqrt(dim), causal)
     assert T.max_abs_error(out["o"], want["o"]) <= tol
     assert T.max_abs_error(out["lse"], want["lse"]) <= 2e-3
+    # Delta = rowsum(dO * O) over the O the forward wrote (already rounded to
+    # the element type), in fp32: within the summation bound of D products
+    o64, do64 = out["o"].astype(np.float64), d_out.astype(np.float64)
+    delta_want = np.sum(do64 * o64, -1)
+    bound = dim * 2.0 ** -23 * np.sum(np.abs(do64 * o64), -1) + 1e-30
+    assert np.all(np.abs(out["delta"] - delta_want) <= bound)
     for name in ("dq", "dk", "dv"):
         assert T.hybrid_error(out[name], want[name]) <= tol, name
 

@@ -334,6 +334,53 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   }
 }
 
+/* ---- backward: Delta ------------------------------------------------------
+ * Delta_i = sum_d dO[i, d] O[i, d] in fp32 (AttentionBackwardKernel.swift:
+ * 119-124).  HBM-bound: each lane loads 16 bytes of O and of dO per row
+ * (D / 8 lanes per row), a wave covers 64 rows with all its loads issued
+ * before the first reduction, and each row reduces over its D / 8 lanes. */
+template <typename T, int D>
+TM_DEV void attn_pre_fast(const TmAttnPreArgs &p) {
+  constexpr int LPR = D / 8;        /* lanes per row */
+  constexpr int RPI = 64 / LPR;     /* rows per wave instruction */
+  constexpr int NI = 64 / RPI;      /* instructions per wave (64 rows) */
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = p.n_ctx;
+  const int nrb = (n + 255) / 256;
+  const int bh = blockIdx.x / nrb;
+  const int r0 = (blockIdx.x - bh * nrb) * 256 + wave * 64 + lane / LPR;
+  const int64_t base = (int64_t)bh * p.stride_head + (lane % LPR) * 8;
+  const T *O = (const T *)p.o + base;
+  const T *dO = (const T *)p.dout + base;
+  u32x4 o[NI], d[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int64_t row = min(r0 + i * RPI, n - 1);
+    o[i] = *(const u32x4 *)(O + row * p.stride_seq);
+    d[i] = *(const u32x4 *)(dO + row * p.stride_seq);
+  }
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const typename Vec8<T>::type ov = as_vec8<T>(o[i]), dv = as_vec8<T>(d[i]);
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(to_f32(ov[e]), to_f32(dv[e]), acc);
+#pragma unroll
+    for (int off = LPR / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    const int row = r0 + i * RPI;
+    if ((lane % LPR) == 0 && row < n) p.delta[(int64_t)bh * p.stride_lse + row] = acc;
+  }
+}
+
+#define TM_PRE_FAST(T, TN, D) \
+  extern "C" __global__ __launch_bounds__(256) void tm_attn_pre_fast_##TN##_d##D(TmAttnPreArgs p) { \
+    attn_pre_fast<T, D>(p); \
+  }
+TM_PRE_FAST(bf16_t, bf16, 64)
+TM_PRE_FAST(bf16_t, bf16, 128)
+TM_PRE_FAST(f16_t, f16, 64)
+TM_PRE_FAST(f16_t, f16, 128)
+
 /* ---- backward: dQ ------------------------------------------------------
  * One workgroup = 4 waves = 128 queries; each wave owns 32 queries and walks
  * the key blocks (64 keys) of its head.  Per block, with the lane owning one

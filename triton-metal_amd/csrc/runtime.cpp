@@ -696,9 +696,14 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         plan.empty = true;
         return plan;
       }
-      plan.variant = format("tm_attn_pre_generic_%s", el);
-      plan.grid[0] = (unsigned)cdiv(p.n_ctx, 64);
-      plan.grid[1] = (unsigned)heads;
+      if (attn_fast_ok(spec, p.stride_head, p.stride_seq, 1.f)) {
+        plan.variant = format("tm_attn_pre_fast_%s_d%d", el, spec.head_dim);
+        plan.grid[0] = (unsigned)(cdiv(p.n_ctx, 256) * heads);
+      } else {
+        plan.variant = format("tm_attn_pre_generic_%s", el);
+        plan.grid[0] = (unsigned)cdiv(p.n_ctx, 64);
+        plan.grid[1] = (unsigned)heads;
+      }
       plan.block = 256;
       set_kernarg(plan, p);
       break;
