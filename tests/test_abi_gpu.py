@@ -194,3 +194,54 @@ def test_builtin_launch_checks_buffer_extents(core, device):
         core.free_buffer(small)
         core.release_kernel(kernel)
         core.release_library(lib)
+
+
+BLOCK_KERNEL = r"""
+#include <hip/hip_runtime.h>
+struct Block { const void *a, *b; void *c; int m, n, k, s0, s1, s2, s3, s4, s5; const void *bias; };
+extern "C" __global__ void block_kernel(Block p) { if (threadIdx.x == 0) ((int *)p.c)[0] = p.m; }
+"""
+
+
+def test_user_launches_must_bind_the_declared_arguments(core, device, tmp_path):
+    """The library reads each user kernel's parameter layout from its code
+    object and refuses a launch that packs another one: the kernel would read
+    its grid size and the rest of its implicit values from the wrong bytes."""
+    library = core.compile_msl(SCALE_BIAS)
+    kernel = core.load_kernel(library, "scale_bias_kernel")
+    bin_, bout = core.alloc_buffer(256), core.alloc_buffer(256)
+    try:
+        with pytest.raises(RuntimeError, match=r"declares 5 arguments \(28 bytes\) but the launch "
+                                               r"binds 3 \(20 bytes\)"):
+            core.launch(kernel, (1, 1, 1), 64, [core.ARG_BUFFER, core.ARG_BUFFER, core.ARG_I32],
+                        [bin_, bout, 4])
+        with pytest.raises(RuntimeError, match=r"argument 2 is 4 bytes at offset 16 \(by_value\) "
+                                               r"but the launch binds 8 bytes at offset 16"):
+            core.launch(kernel, (1, 1, 1), 64,
+                        [core.ARG_BUFFER, core.ARG_BUFFER, core.ARG_I64, core.ARG_F32, core.ARG_I32],
+                        [bin_, bout, 1, core.float_bits(1.0), 4])
+    finally:
+        core.free_buffer(bin_)
+        core.free_buffer(bout)
+        core.release_kernel(kernel)
+        core.release_library(library)
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    src = tmp_path / "block.hip"
+    src.write_text(BLOCK_KERNEL)
+    image_path = tmp_path / "block.hsaco"
+    subprocess.run([hipcc, "--offload-arch=gfx950", "--genco", "-O2", str(src), "-o",
+                    str(image_path)], check=True, timeout=120)
+    library = core.load_metallib(image_path.read_bytes())
+    kernel = core.load_kernel(library, "block_kernel")
+    out = core.alloc_buffer(64)
+    try:
+        # the reference's 12 matmul arguments against one 72-byte by-value block
+        with pytest.raises(RuntimeError, match=r"declares 1 argument \(72 bytes\) but the launch "
+                                               r"binds 12 \(60 bytes\)"):
+            core.launch(kernel, (1, 1, 1), 64, [core.ARG_BUFFER] * 3 + [core.ARG_I32] * 9,
+                        [out, out, out] + [7] * 9)
+    finally:
+        core.free_buffer(out)
+        core.release_kernel(kernel)
+        core.release_library(library)

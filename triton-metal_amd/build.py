@@ -81,7 +81,7 @@ def build(jobs: int = 8) -> Path:
     _run([
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
         "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}",
-        str(CSRC / "runtime.cpp"), str(blobs),
+        str(CSRC / "runtime.cpp"), str(CSRC / "codeobject.cpp"), str(blobs),
         "-o", str(LIBRARY),
         f"-L{ROCM / 'lib'}", "-lamdhip64", "-lhiprtc", f"-Wl,-rpath,{ROCM / 'lib'}",
     ])

@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -39,6 +40,7 @@
 #include <unordered_map>
 #include <vector>
 
+#include "codeobject.h"
 #include "tm_args.h"
 
 namespace {
@@ -212,6 +214,9 @@ struct Library : Object {
   bool builtin = false;
   BuiltinSpec spec;
   hipModule_t module = nullptr; /* user code object (not built-in) */
+  /* explicit parameters of each kernel, from the code object's metadata
+   * (empty when the image carries none this library can read) */
+  std::map<std::string, std::vector<tm_codeobject::ArgSlot>> signatures;
   ~Library() override {
     if (module) (void)hipModuleUnload(module);
   }
@@ -225,6 +230,8 @@ struct Kernel : Object {
   std::string name;
   Builtin builtin = Builtin::None;
   hipFunction_t function = nullptr; /* user kernels */
+  bool has_signature = false;                     /* user kernels: declared parameters known */
+  std::vector<tm_codeobject::ArgSlot> signature;
   std::mutex lock;
   std::string last_variant;
 };
@@ -802,6 +809,28 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
 /* User kernels: pack the arguments with natural alignment (pointers and i64 on
  * 8 bytes, i32 and f32 on 4) — the AMDGPU kernarg layout of a kernel whose
  * parameters are declared in the same order. */
+/* A user launch must bind exactly the parameters the kernel declares, at the
+ * same offsets and sizes: the kernel reads its implicit values (grid size,
+ * workgroup size) from fixed offsets after them, so any other layout would
+ * make it read garbage on the GPU. */
+void check_signature_layout(const Kernel &k, const std::vector<std::pair<long, long>> &packed) {
+  const auto &want = k.signature;
+  long want_bytes = 0, have_bytes = 0;
+  for (const auto &a : want) want_bytes = std::max(want_bytes, a.offset + a.size);
+  for (const auto &a : packed) have_bytes = std::max(have_bytes, a.first + a.second);
+  if (want.size() != packed.size())
+    throw TmError(format("kernel '%s' declares %zu argument%s (%ld bytes) but the launch binds "
+                         "%zu (%ld bytes)",
+                         k.name.c_str(), want.size(), want.size() == 1 ? "" : "s", want_bytes,
+                         packed.size(), have_bytes));
+  for (size_t i = 0; i < want.size(); ++i)
+    if (want[i].offset != packed[i].first || want[i].size != packed[i].second)
+      throw TmError(format("kernel '%s' argument %zu is %ld bytes at offset %ld (%s) but the "
+                           "launch binds %ld bytes at offset %ld",
+                           k.name.c_str(), i, want[i].size, want[i].offset, want[i].kind.c_str(),
+                           packed[i].second, packed[i].first));
+}
+
 Plan plan_user(Kernel &k, const std::vector<Arg> &args, int64_t gx, int64_t gy, int64_t gz,
                int64_t threads) {
   Plan plan;
@@ -813,11 +842,13 @@ Plan plan_user(Kernel &k, const std::vector<Arg> &args, int64_t gx, int64_t gy, 
   plan.grid[2] = (unsigned)gz;
   plan.block = (unsigned)threads;
   auto &buf = plan.kernarg;
-  auto put = [&buf](const void *src, size_t size) {
+  std::vector<std::pair<long, long>> packed; /* (offset, size) of each bound argument */
+  auto put = [&buf, &packed](const void *src, size_t size) {
     while (buf.size() % size) buf.push_back(0);
     const size_t at = buf.size();
     buf.resize(at + size);
     memcpy(buf.data() + at, src, size);
+    packed.emplace_back((long)at, (long)size);
   };
   for (const Arg &a : args) {
     switch (a.kind) {
@@ -844,6 +875,7 @@ Plan plan_user(Kernel &k, const std::vector<Arg> &args, int64_t gx, int64_t gy, 
     }
   }
   while (buf.size() % 8) buf.push_back(0);
+  if (k.has_signature) check_signature_layout(k, packed);
   return plan;
 }
 
@@ -1114,6 +1146,7 @@ int64_t tm_compile_msl(const char *source) {
     std::vector<char> code = compile_hip_source(source);
     require_device();
     hip_check(hipModuleLoadData(&lib->module, code.data()), "could not load compiled HIP code");
+    lib->signatures = tm_codeobject::read_kernel_arguments(code.data(), code.size());
   }
   return handles().insert(lib);
   TM_GUARD_END(0)
@@ -1133,6 +1166,7 @@ int64_t tm_load_metallib(const void *image, int64_t length) {
                          "object (%s)",
                          hipGetErrorName(status)));
   }
+  lib->signatures = tm_codeobject::read_kernel_arguments(copy.data(), copy.size());
   return handles().insert(lib);
   TM_GUARD_END(0)
 }
@@ -1164,6 +1198,11 @@ int64_t tm_load_kernel(int64_t library, const char *name) {
       (void)hipGetLastError();
       throw TmError(format("kernel '%s' not found in library (%s)", name,
                            hipGetErrorName(status)));
+    }
+    const auto sig = lib->signatures.find(name);
+    if (sig != lib->signatures.end()) {
+      k->has_signature = true;
+      k->signature = sig->second;
     }
   }
   return handles().insert(k);
