@@ -241,6 +241,14 @@ def test_user_launches_must_bind_the_declared_arguments(core, device, tmp_path):
                                                r"binds 12 \(60 bytes\)"):
             core.launch(kernel, (1, 1, 1), 64, [core.ARG_BUFFER] * 3 + [core.ARG_I32] * 9,
                         [out, out, out] + [7] * 9)
+        # a by-value struct may be bound field by field, in order (13 fields, 72 bytes)
+        core.launch(kernel, (1, 1, 1), 64, [core.ARG_BUFFER] * 3 + [core.ARG_I32] * 9 + [core.ARG_I64],
+                    [out, out, out] + [7] * 9 + [0])
+        assert _download(core, out, 1, "i")[0] == 7
+        # one argument that covers only the start of the block
+        with pytest.raises(RuntimeError, match=r"argument 0 is 72 bytes at offset 0 \(by_value\) "
+                                               r"but the launch binds 8 bytes at offset 0"):
+            core.launch(kernel, (1, 1, 1), 64, [core.ARG_I64], [0])
     finally:
         core.free_buffer(out)
         core.release_kernel(kernel)

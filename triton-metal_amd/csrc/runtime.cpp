@@ -809,26 +809,40 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
 /* User kernels: pack the arguments with natural alignment (pointers and i64 on
  * 8 bytes, i32 and f32 on 4) — the AMDGPU kernarg layout of a kernel whose
  * parameters are declared in the same order. */
-/* A user launch must bind exactly the parameters the kernel declares, at the
- * same offsets and sizes: the kernel reads its implicit values (grid size,
- * workgroup size) from fixed offsets after them, so any other layout would
- * make it read garbage on the GPU. */
+/* A user launch must bind the parameter layout the kernel declares: each
+ * declared parameter is covered exactly by one bound argument, or (a by-value
+ * struct bound field by field, in order) by a run of them, with no argument
+ * straddling a parameter boundary.  The kernel reads its implicit values (grid
+ * size, workgroup size) from fixed offsets after its parameters, so any other
+ * layout would make it read garbage on the GPU. */
 void check_signature_layout(const Kernel &k, const std::vector<std::pair<long, long>> &packed) {
   const auto &want = k.signature;
   long want_bytes = 0, have_bytes = 0;
   for (const auto &a : want) want_bytes = std::max(want_bytes, a.offset + a.size);
   for (const auto &a : packed) have_bytes = std::max(have_bytes, a.first + a.second);
-  if (want.size() != packed.size())
+  size_t j = 0;
+  long bad = -1; /* first declared parameter the launch does not cover */
+  for (size_t i = 0; i < want.size() && bad < 0; ++i) {
+    const long at = want[i].offset, end = at + want[i].size;
+    if (j >= packed.size() || packed[j].first != at) {
+      bad = (long)i;
+      break;
+    }
+    const size_t first = j;
+    while (j < packed.size() && packed[j].first + packed[j].second <= end) ++j;
+    if (j == first || packed[j - 1].first + packed[j - 1].second != end) bad = (long)i;
+  }
+  if (bad < 0 && j == packed.size()) return;
+  if (want.size() != packed.size() || bad < 0)
     throw TmError(format("kernel '%s' declares %zu argument%s (%ld bytes) but the launch binds "
                          "%zu (%ld bytes)",
                          k.name.c_str(), want.size(), want.size() == 1 ? "" : "s", want_bytes,
                          packed.size(), have_bytes));
-  for (size_t i = 0; i < want.size(); ++i)
-    if (want[i].offset != packed[i].first || want[i].size != packed[i].second)
-      throw TmError(format("kernel '%s' argument %zu is %ld bytes at offset %ld (%s) but the "
-                           "launch binds %ld bytes at offset %ld",
-                           k.name.c_str(), i, want[i].size, want[i].offset, want[i].kind.c_str(),
-                           packed[i].second, packed[i].first));
+  const size_t i = (size_t)bad;
+  throw TmError(format("kernel '%s' argument %zu is %ld bytes at offset %ld (%s) but the launch "
+                       "binds %ld bytes at offset %ld",
+                       k.name.c_str(), i, want[i].size, want[i].offset, want[i].kind.c_str(),
+                       packed[i].second, packed[i].first));
 }
 
 Plan plan_user(Kernel &k, const std::vector<Arg> &args, int64_t gx, int64_t gy, int64_t gz,
