@@ -200,6 +200,9 @@ BLOCK_KERNEL = r"""
 #include <hip/hip_runtime.h>
 struct Block { const void *a, *b; void *c; int m, n, k, s0, s1, s2, s3, s4, s5; const void *bias; };
 extern "C" __global__ void block_kernel(Block p) { if (threadIdx.x == 0) ((int *)p.c)[0] = p.m; }
+/* 28 bytes of fields, 4 bytes of tail padding */
+struct Tail { const void *a; void *b; int m, n, k; };
+extern "C" __global__ void tail_kernel(Tail p) { if (threadIdx.x == 0) ((int *)p.b)[0] = p.m + p.n + p.k; }
 """
 
 
@@ -249,6 +252,18 @@ def test_user_launches_must_bind_the_declared_arguments(core, device, tmp_path):
         with pytest.raises(RuntimeError, match=r"argument 0 is 72 bytes at offset 0 \(by_value\) "
                                                r"but the launch binds 8 bytes at offset 0"):
             core.launch(kernel, (1, 1, 1), 64, [core.ARG_I64], [0])
+        # a struct whose fields stop short of its size by tail padding only
+        tail = core.load_kernel(library, "tail_kernel")
+        try:
+            core.launch(tail, (1, 1, 1), 64, [core.ARG_BUFFER] * 2 + [core.ARG_I32] * 3,
+                        [out, out, 1, 20, 300])
+            assert _download(core, out, 1, "i")[0] == 321
+            with pytest.raises(RuntimeError, match=r"declares 1 argument \(32 bytes\) but the launch "
+                                                   r"binds 4 \(24 bytes\)"):
+                core.launch(tail, (1, 1, 1), 64, [core.ARG_BUFFER] * 2 + [core.ARG_I32] * 2,
+                            [out, out, 1, 20])
+        finally:
+            core.release_kernel(tail)
     finally:
         core.free_buffer(out)
         core.release_kernel(kernel)

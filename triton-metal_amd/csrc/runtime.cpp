@@ -830,7 +830,17 @@ void check_signature_layout(const Kernel &k, const std::vector<std::pair<long, l
     }
     const size_t first = j;
     while (j < packed.size() && packed[j].first + packed[j].second <= end) ++j;
-    if (j == first || packed[j - 1].first + packed[j - 1].second != end) bad = (long)i;
+    if (j == first) {
+      bad = (long)i;
+      break;
+    }
+    const long covered = packed[j - 1].first + packed[j - 1].second;
+    /* a by-value struct bound field by field may stop short of its size by its
+     * tail padding (less than its 8-byte alignment); the packed block is
+     * padded to 8 bytes, so the kernel's implicit values stay in place */
+    const bool tail_padding = want[i].kind == "by_value" && want[i].size > 8 && end % 8 == 0 &&
+                              end - covered < 8;
+    if (covered != end && !tail_padding) bad = (long)i;
   }
   if (bad < 0 && j == packed.size()) return;
   if (want.size() != packed.size() || bad < 0)
