@@ -16,9 +16,10 @@ Also measured in the same run and reported under "components":
 Per-kernel durations come from HIP events recorded on the library's stream
 around back-to-back dispatches (tm_launch_timed).
 
-The CPU baseline times a numpy port of the reference's attention forward and
-backward (attention_training.py:170-187, causal) on a bounded sample of the
-workload on the host cores.
+The CPU baseline times the oracle's float32 BLAS restatement of the reference's
+attention forward and backward (oracle/reference.py attention_head_f32, after
+attention_training.py:170-187, causal) on a bounded sample of the workload on
+the host cores.
 Prints ONE JSON line.
 """
 
@@ -224,36 +225,24 @@ def bench_sae(core, ops, rows, model, features, warmup, sample_ms):
 
 
 def cpu_baseline(target_seconds):
-    """numpy (fp32 BLAS) causal attention forward + backward, one (batch, head)
-    of config 5 at a time (S=4096, D=128), repeated until about
-    `target_seconds` of CPU work; TFLOP/s under the same FLOP convention.  The
-    per-head body is the reference's numpy forward and backward
-    (python/examples/attention_training.py:170-187) with the causal mask."""
+    """The oracle's float32 BLAS restatement of the reference's attention forward
+    and backward (oracle.reference.attention_head_f32; attention_training.py:
+    170-187 with the causal mask), one (batch, head) of config 5 at a time
+    (S=4096, D=128), repeated until about `target_seconds` of CPU work; TFLOP/s
+    under the same FLOP convention."""
+    from oracle import reference as R  # the CPU baseline is the oracle, timed
 
     seq, dim = 4096, 128
     scale = np.float32(1 / math.sqrt(dim))
     rng = np.random.default_rng(0)
-    mask = np.triu(np.ones((seq, seq), dtype=bool), 1)
 
     def one_head(q, k, v, d_out):
-        s = (q @ k.T) * scale
-        s[mask] = -np.inf
-        s -= s.max(-1, keepdims=True)
-        p = np.exp(s)
-        p /= p.sum(-1, keepdims=True)
-        o = p @ v
-        dv = p.T @ d_out
-        dp = d_out @ v.T
-        delta = np.sum(d_out * o, -1, keepdims=True)
-        ds = p * (dp - delta)
-        dq = (ds @ k) * scale
-        dk = (ds.T @ q) * scale
-        return o, dq, dk, dv
+        return R.attention_head_f32(q, k, v, d_out, scale, causal=True)
 
+    q, k, v, d_out = (rng.standard_normal((seq, dim), dtype=np.float32) for _ in range(4))
     heads = 0
     t0 = time.perf_counter()
     while True:
-        q, k, v, d_out = (rng.standard_normal((seq, dim), dtype=np.float32) for _ in range(4))
         one_head(q, k, v, d_out)
         heads += 1
         elapsed = time.perf_counter() - t0

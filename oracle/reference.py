@@ -6,12 +6,14 @@ attention_forward    O, P, L (log2 units)               AttentionTests.swift:21-
                                                         AttentionKernel.swift:33-39 (L = m + log2 l)
 attention_backward   Delta, dQ, dK, dV, amplification   AttentionBackwardTests.swift:46-160;
                                                         attention_training.py:179-187
+attention_head_f32   one head's fwd + bwd via BLAS        attention_training.py:170-187 (the CPU baseline)
 sae_encode           relu(x @ W_enc + b_enc)            SAEEncoder.swift:1-20;
                                                         sae_encode.py:60-61 (numpy reference)
 The causal mask (key j > query i excluded) is this build's extension; the
 reference has none.  Arrays are [heads, seq, dim].
 """
 
+import functools
 import math
 
 import numpy as np
@@ -113,6 +115,39 @@ def numpy_attention_backward_f32(q, k, v, weights, d_out, scale):
     dq = np.einsum("hij,hjd->hid", ds, k) * scale
     dk = np.einsum("hij,hid->hjd", ds, q) * scale
     return dq, dk, dv
+
+
+@functools.lru_cache(maxsize=4)
+def _causal_bias(rows, cols):
+    """float32 [rows, cols]: 0 where key j <= query i, -inf above the diagonal."""
+    bias = np.zeros((rows, cols), np.float32)
+    bias[np.triu_indices(rows, 1, cols)] = -np.inf
+    return bias
+
+
+def attention_head_f32(q, k, v, d_out, scale, causal=False):
+    """One head's forward and backward in float32 through BLAS matmuls: the
+    arithmetic of numpy_attention_f32 and numpy_attention_backward_f32
+    (attention_training.py:170-187) with `@` in place of einsum and Delta as
+    rowsum(dO * O), plus the causal mask (keys after the query excluded).  [S, D] inputs; returns
+    (O, dQ, dK, dV).  This is what the benchmark's CPU baseline times."""
+    scale = np.float32(scale)
+    s = (q @ k.T) * scale
+    if causal:
+        s += _causal_bias(s.shape[0], s.shape[1])
+    s -= s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(-1, keepdims=True)
+    o = p @ v
+    dv = p.T @ d_out
+    dp = d_out @ v.T
+    # rowsum(dP * P) as the reference writes it equals rowsum(dO * O), an [S, D]
+    # product instead of an [S, S] one (the FlashAttention-2 Delta)
+    delta = (d_out * o).sum(-1, keepdims=True)
+    ds = p * (dp - delta)
+    dq = (ds @ k) * scale
+    dk = (ds.T @ q) * scale
+    return o, dq, dk, dv
 
 
 def reference_training_inputs(heads=2, seq=96, dim=64, seed=0, spread=0.5):

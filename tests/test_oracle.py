@@ -175,6 +175,24 @@ def test_sae_oracle_against_brute_force_and_relu_properties():
     assert np.array_equal(z, np.tile(np.maximum(b.astype(np.float64), 0), (3, 1)))
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_blas_head_restatement_matches_the_reference_numpy_and_fp64(causal):
+    # The CPU baseline's BLAS form equals the reference's einsum form (non-causal)
+    # and the fp64 oracle (both), at float32 accuracy.
+    rng = np.random.default_rng(3)
+    q, k, v, d_out = (rng.standard_normal((1, 40, 16), dtype=np.float32) for _ in range(4))
+    scale = 0.25
+    o, dq, dk, dv = R.attention_head_f32(q[0], k[0], v[0], d_out[0], scale, causal)
+    if not causal:
+        o_ref, w = R.numpy_attention_f32(q, k, v, np.float32(scale))
+        dq_ref, dk_ref, dv_ref = R.numpy_attention_backward_f32(q, k, v, w, d_out, np.float32(scale))
+        for got, want in ((o, o_ref), (dq, dq_ref), (dk, dk_ref), (dv, dv_ref)):
+            assert np.allclose(got, want[0], rtol=1e-4, atol=1e-5)
+    want = R.attention_backward(q, k, v, d_out, scale, causal)
+    for got, name in ((o, "o"), (dq, "dq"), (dk, "dk"), (dv, "dv")):
+        assert np.allclose(got, want[name][0], rtol=1e-4, atol=1e-5), name
+
+
 def test_tolerance_metrics():
     assert T.hybrid_error([1.0, 10.0], [1.0, 11.0]) == pytest.approx(1 / 11)
     assert T.hybrid_error([0.5], [0.0]) == pytest.approx(0.5)
