@@ -259,3 +259,39 @@ def test_bf16_conversion_rounds_to_nearest_even():
     assert np.isinf(bf16_values(bits)[5])
     assert np.isnan(bf16_values(bf16_bits(np.array([np.nan], np.float32))))[0]
     assert np.array_equal(bf16_values(bf16_bits(bf16_values(bits))), bf16_values(bits))
+
+
+def test_handle_table_is_safe_under_concurrent_use(core):
+    """The handle table is one locked table shared by every thread (the
+    reference's Runtime.swift:250-290): concurrent create/load/release from
+    several threads yields unique handles, every release succeeds, and the live
+    count returns to where it started."""
+    import threading
+
+    names = ("matmul_kernel", "attn_fwd", "attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv",
+             "sae_encode_kernel")
+    live = core.live_handle_count()
+    seen, errors, lock = [], [], threading.Lock()
+
+    def worker(seed):
+        try:
+            for i in range(60):
+                spec = f"builtin element={('f32', 'f16', 'bf16')[(seed + i) % 3]} head_dim=64"
+                lib = core.compile_msl(spec)
+                kernels = [core.load_kernel(lib, n) for n in names]
+                with lock:
+                    seen.extend([lib] + kernels)
+                for k in kernels:
+                    core.release_kernel(k)
+                core.release_library(lib)
+        except Exception as exc:  # surfaced below
+            errors.append(repr(exc))
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(8)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors[:3]
+    assert len(seen) == len(set(seen)) == 8 * 60 * 7
+    assert core.live_handle_count() == live

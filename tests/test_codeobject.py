@@ -96,3 +96,52 @@ def test_truncated_and_foreign_images_yield_nothing(built):
                                          "takes_block"}
     (built / "junk.bin").write_bytes(bytes(range(256)) * 64)
     assert read(built, built / "junk.bin") == {}
+
+
+FUZZ = r"""
+#include <cstdio>
+#include <fstream>
+#include <iterator>
+#include <random>
+#include <vector>
+#include "codeobject.h"
+int main(int argc, char **argv) {
+  long total = 0;
+  for (int f = 1; f < argc; ++f) {
+    std::ifstream in(argv[f], std::ios::binary);
+    std::vector<char> img((std::istreambuf_iterator<char>(in)), std::istreambuf_iterator<char>());
+    for (size_t n = 0; n <= img.size(); n += 3) {
+      std::vector<char> cut(img.begin(), img.begin() + n);
+      total += tm_codeobject::read_kernel_arguments(cut.data(), cut.size()).size();
+    }
+    std::mt19937 rng(f);
+    for (int it = 0; it < 2000; ++it) {
+      std::vector<char> mut = img;
+      for (int k = 0, flips = 1 + rng() % 8; k < flips; ++k) mut[rng() % mut.size()] = (char)rng();
+      total += tm_codeobject::read_kernel_arguments(mut.data(), mut.size()).size();
+    }
+  }
+  std::printf("parsed %ld\n", total);
+  return 0;
+}
+"""
+
+
+def test_reader_survives_truncated_and_corrupted_images_under_sanitizers(built):
+    """Every truncation of a bundle and of a raw ELF, and 2000 random byte
+    corruptions of each, through the reader built with AddressSanitizer and
+    UndefinedBehaviorSanitizer (host code only): no out-of-bounds read, no
+    undefined behaviour, whatever the bytes."""
+    (built / "fuzz.cpp").write_text(FUZZ)
+    exe = built / "fuzz"
+    build = subprocess.run(["g++", "-O1", "-g", "-fsanitize=address,undefined",
+                            "-fno-sanitize-recover=all", "-std=c++17", f"-I{CSRC}",
+                            str(built / "fuzz.cpp"), str(CSRC / "codeobject.cpp"), "-o", str(exe)],
+                           capture_output=True, text=True)
+    if build.returncode != 0:
+        pytest.skip("g++ cannot build with -fsanitize=address,undefined here: " + build.stderr[-200:])
+    run = subprocess.run([str(exe), str(built / "bundle.hsaco"), str(built / "raw.o")],
+                         capture_output=True, text=True, timeout=300,
+                         env={"ASAN_OPTIONS": "detect_leaks=0"})
+    assert run.returncode == 0, run.stderr[-2000:]
+    assert run.stdout.startswith("parsed ")

@@ -72,6 +72,26 @@ def write_blobs(images):
     return path
 
 
+def build_sanitized() -> Path:
+    """The host library alone (runtime + code-object reader, kernels as built)
+    under AddressSanitizer and UndefinedBehaviorSanitizer, for CPU test runs:
+        LD_PRELOAD="$(gcc -print-file-name=libasan.so) $(gcc -print-file-name=libubsan.so)" \\
+        ASAN_OPTIONS=detect_leaks=0 TRITON_METAL_CORE_LIB=<this file> pytest tests -m "not gpu"
+    Host code only: the kernels are the normal gfx950 builds."""
+    blobs = LIB / "blobs.S"
+    if not blobs.exists():
+        build()
+    out = LIB / "libtritonmetal_asan.so"
+    _run([
+        "g++", "-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
+        "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}",
+        str(CSRC / "runtime.cpp"), str(CSRC / "codeobject.cpp"), str(blobs),
+        "-o", str(out),
+        f"-L{ROCM / 'lib'}", "-lamdhip64", "-lhiprtc", f"-Wl,-rpath,{ROCM / 'lib'}",
+    ])
+    return out
+
+
 def build(jobs: int = 8) -> Path:
     LIB.mkdir(exist_ok=True)
     srcs = kernel_sources()
@@ -91,6 +111,10 @@ def build(jobs: int = 8) -> Path:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
+    ap.add_argument("--sanitize", action="store_true",
+                    help="also build lib/libtritonmetal_asan.so (host code under ASan + UBSan)")
     args = ap.parse_args()
     print(build(args.jobs))
+    if args.sanitize:
+        print(build_sanitized())
     sys.exit(0)
