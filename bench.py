@@ -3,15 +3,15 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 
 A step is one FlashAttention-2 forward + backward (attn_fwd, attn_bwd_preprocess,
-attn_bwd_dq, attn_bwd_dkdv) at BASELINE config 5: bf16, B4 H32 S4096 D128,
+attn_bwd_dq, attn_bwd_dkdv) at the benchmark's config 5: bf16, B4 H32 S4096 D128,
 causal, Q/K/V/dO ~ N(0,1), inputs resident in HBM.  `value` is that step's
 algorithmic TFLOP/s under the reference's FLOP convention (4*S^2*D forward,
 10*S^2*D backward per batch*head, AttentionBenchmark.swift:64-68,
 AttentionBackwardBenchmark.swift:45-49), halved for the causal mask.
 
 Also measured in the same run and reported under "components":
-  - bf16 GEMM 8192^3 (BASELINE config 3), 2*M*N*K FLOPs;
-  - bf16 FA2 forward at B8 H16 S1024 D64 non-causal (BASELINE config 4);
+  - bf16 GEMM 8192^3 (config 3), 2*M*N*K FLOPs;
+  - bf16 FA2 forward at B8 H16 S1024 D64 non-causal (config 4);
   - the fused bf16 SAE encoder relu(x @ W_enc + b_enc) at 8192 x 2048 x 16384.
 Per-kernel durations come from HIP events recorded on the library's stream
 around back-to-back dispatches (tm_launch_timed).
@@ -342,7 +342,7 @@ def main():
                       "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS["bf16"], 4),
                       "traffic": measured_traffic(kernels[dominant]["variant"])})
 
-        # forward only, B8 H16 S1024 D64 non-causal.
+        # config 4: forward only, B8 H16 S1024 D64 non-causal.
         _, k4 = bench_attention(core, ops, 8, 16, 1024, 64, False, 0, args.warmup,
                                 args.sample_ms, backward=False)
         f4 = attention_flops(8 * 16, 1024, 64, False)
@@ -385,10 +385,10 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic N(0,1) bf16 inputs, resident in HBM",
-        "config": {"workload": "fa2_fwd_bwd_bf16_causal (BASELINE config 5)", "batch": 4,
+        "config": {"workload": "fa2_fwd_bwd_bf16_causal (config 5)", "batch": 4,
                    "heads": 32, "seq_len": 4096, "head_dim": 128, "causal": True,
                    "parallelism": "none (1 GPU)"} if args.only != "gemm" else
-                  {"workload": "gemm_bf16_8192 (BASELINE config 3)", "m": 8192, "n": 8192,
+                  {"workload": "gemm_bf16_8192 (config 3)", "m": 8192, "n": 8192,
                    "k": 8192, "parallelism": "none (1 GPU)"},
         "roofline": result.get("roofline"),
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),

@@ -2,7 +2,7 @@
 
 Mirrors Tests/TritonMetalCoreTests/AttentionTests.swift:119-206 and
 AttentionBackwardTests.swift:330-575, python/examples/attention_training.py
-and BASELINE configs 4 and 5 at full size.  Tolerances:
+(benchmark config 2) and configs 4 and 5 at full size.  Tolerances:
 the reference's own (2e-5 hybrid for f32 forward, 4e-3 for f16 forward, the
 derived summation bound n*u*A for the backward) and the north star's 2e-2
 absolute against an fp32-or-better reference for bf16.
@@ -213,7 +213,7 @@ def test_gradients_at_every_requested_workgroup_size(device, threads):
 
 
 # --------------------------------------------------------------------------- #
-# the attention training run
+# Config 2: the attention training run
 # --------------------------------------------------------------------------- #
 
 
@@ -250,7 +250,7 @@ def test_published_training_run_on_the_device(device):
 
 
 def test_config2_training_steps_match_numpy_autograd(device):
-    """B1 H2 S96 D64 fp32, Q/K/V/W ~ N(0, 0.1), scale 1/8,
+    """Config 2: B1 H2 S96 D64 fp32, Q/K/V/W ~ N(0, 0.1), scale 1/8,
     forward + backward + 8 SGD steps at lr 1e-3 on the sum-of-squares loss
     0.5*||O - W||^2 (W read as the regression target), every step within 1e-5
     relative of the fp64 numpy autograd run from the same inputs."""
@@ -275,7 +275,7 @@ def test_config2_training_steps_match_numpy_autograd(device):
 
 
 # --------------------------------------------------------------------------- #
-# BASELINE configs 4 and 5 at full size
+# Configs 4 and 5 at full size
 # --------------------------------------------------------------------------- #
 
 

@@ -1,5 +1,5 @@
 """matmul_kernel on the device against the oracle (reference DotTests.swift:318-646,
-python/examples/matmul.py:66-79) and BASELINE configs 1 and 3.
+python/examples/matmul.py:66-79) and benchmark configs 1 and 3.
 
 Tolerance metric: the reference's |a - b| / max(1, |b|) (GPUHarness.swift:146),
 with the reference computed from inputs already rounded to the element type
@@ -137,7 +137,7 @@ def test_numpy_tutorial_known_answer(device):
 
 
 def test_config1_fp32_256_uniform(device):
-    """fp32 256^3, U[-1,1] from seed 0, 1e-5 (hybrid) vs fp64."""
+    """Config 1: fp32 256^3, U[-1,1] from seed 0, 1e-5 (hybrid) vs fp64."""
     a = G.uniform((256, 256), seed=0)
     b = G.uniform((256, 256), seed=1)
     c, _ = run_matmul(a.reshape(-1), b.reshape(-1), 256, 256, 256, (256, 1, 256, 1, 256, 1))
@@ -160,7 +160,7 @@ def test_large_aligned_gemm_hybrid_and_checksums(device, element):
 
 
 def test_config3_bf16_8192_cube(device):
-    """bf16 8192^3, N(0,1) from seed, f32 accumulate, bf16 out.
+    """Config 3: bf16 8192^3, N(0,1) from seed, f32 accumulate, bf16 out.
     Full size: 256 sampled rows against fp64 (from the bf16-rounded inputs) under
     the 2e-2 hybrid metric, and the column-sum checksum over all rows."""
     m = n = k = 8192
