@@ -134,12 +134,16 @@ def kernel_ms(core, kernel, grid, kinds, values, sample_ms):
 
 
 def bench_attention(core, ops, batch, heads, seq, dim, causal, steps, warmup, sample_ms,
-                    backward=True):
+                    backward=True, element="bf16"):
     bh = batch * heads
-    layer = ops.AttentionLayer(bh, seq, dim, "bf16", causal)
+    layer = ops.AttentionLayer(bh, seq, dim, element, causal)
     try:
         for i, name in enumerate(("q", "k", "v", "do")):
-            layer.buffers[name].write(normal_bf16((bh, seq, dim), 100 + i))
+            x = normal_bf16((bh, seq, dim), 100 + i)
+            if element != "bf16":
+                from triton_metal.buffer import bf16_values
+                x = bf16_values(x)  # the same N(0,1) values, converted by write()
+            layer.buffers[name].write(x)
         kern = layer.lib.kernels
         launches = [("attn_fwd", layer.fwd_args(True))]
         if backward:
@@ -171,13 +175,18 @@ def bench_attention(core, ops, batch, heads, seq, dim, causal, steps, warmup, sa
     return wall_ms, per_kernel
 
 
-def bench_gemm(core, ops, n, warmup, sample_ms):
-    from triton_metal.buffer import DeviceBuffer
-    a = DeviceBuffer((n, n), "bfloat16").write(normal_bf16((n, n), 1))
-    b = DeviceBuffer((n, n), "bfloat16").write(normal_bf16((n, n), 2))
-    c = DeviceBuffer((n, n), "bfloat16")
+def bench_gemm(core, ops, n, warmup, sample_ms, element="bf16"):
+    from triton_metal.buffer import DeviceBuffer, bf16_values
+    dtype = {"bf16": "bfloat16", "f16": "float16"}[element]
+
+    def operand(seed):
+        x = normal_bf16((n, n), seed)
+        return DeviceBuffer((n, n), dtype).write(x if element == "bf16" else bf16_values(x))
+
+    a, b = operand(1), operand(2)
+    c = DeviceBuffer((n, n), dtype)
     try:
-        kernel = ops.library("bf16").kernels["matmul_kernel"]
+        kernel = ops.library(element).kernels["matmul_kernel"]
         grid, kinds, values = ops.matmul_args(a, b, c, n, n, n)
         for _ in range(warmup):
             core.launch_async(kernel, grid, 128, kinds, values)
@@ -350,6 +359,16 @@ def main():
         components["fa2_fwd_config4"] = {"tflops": round(f4 / (ms4 * 1e-3) / 1e12, 2),
                                          "frac_of_peak": round(f4 / (ms4 * 1e-3) / 1e12 / 2500, 4),
                                          "ms": round(ms4, 4), "variant": k4["attn_fwd"]["variant"]}
+        # fp16 variant of config 5 (the reference's own attention element type)
+        _, k16 = bench_attention(core, ops, B, H, S, D, True, 0, args.warmup, args.sample_ms,
+                                 element="f16")
+        ms_f = k16["attn_fwd"]["ms"]
+        ms_b = sum(k16[n]["ms"] for n in ("attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv"))
+        components["fa2_f16_config5"] = {
+            "fwd_tflops": round(f_fwd / (ms_f * 1e-3) / 1e12, 2),
+            "bwd_tflops": round(f_bwd / (ms_b * 1e-3) / 1e12, 2),
+            "fwd_ms": round(ms_f, 4), "bwd_ms": round(ms_b, 4),
+            "variants": [k16[n]["variant"] for n in k16]}
     if args.only in ("all", "gemm"):
         n = 8192
         ms, variant = bench_gemm(core, ops, n, args.warmup, args.sample_ms)
@@ -357,6 +376,11 @@ def main():
         components["gemm_bf16_8192"] = {"tflops": round(tf, 2),
                                         "frac_of_peak": round(tf / 2500, 4),
                                         "ms": round(ms, 4), "variant": variant}
+        ms16, variant16 = bench_gemm(core, ops, n, args.warmup, args.sample_ms, element="f16")
+        tf16 = gemm_flops(n, n, n) / (ms16 * 1e-3) / 1e12
+        components["gemm_f16_8192"] = {"tflops": round(tf16, 2),
+                                       "frac_of_peak": round(tf16 / 2500, 4),
+                                       "ms": round(ms16, 4), "variant": variant16}
         # The fused SAE encoder at an 8x dictionary over 8192 tokens of width 2048.
         rows, model, features = 8192, 2048, 16384
         ms_s, variant_s = bench_sae(core, ops, rows, model, features, args.warmup,
