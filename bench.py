@@ -55,7 +55,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the baseline sample")
-    ap.add_argument("--only", choices=["all", "fa", "gemm"], default="all")
+    ap.add_argument("--only", choices=["all", "fa", "gemm", "reference"], default="all")
     ap.add_argument("--probes", action="store_true",
                     help="print the device probe rates (MFMA shapes, exp2, LDS reads, fp32 atomics) "
                          "as one JSON line and exit")
@@ -177,7 +177,7 @@ def bench_attention(core, ops, batch, heads, seq, dim, causal, steps, warmup, sa
 
 def bench_gemm(core, ops, n, warmup, sample_ms, element="bf16"):
     from triton_metal.buffer import DeviceBuffer, bf16_values
-    dtype = {"bf16": "bfloat16", "f16": "float16"}[element]
+    dtype = {"bf16": "bfloat16", "f16": "float16", "f32": "float32"}[element]
 
     def operand(seed):
         x = normal_bf16((n, n), seed)
@@ -369,6 +369,26 @@ def main():
             "bwd_tflops": round(f_bwd / (ms_b * 1e-3) / 1e12, 2),
             "fwd_ms": round(ms_f, 4), "bwd_ms": round(ms_b, 4),
             "variants": [k16[n]["variant"] for n in k16]}
+    if args.only in ("all", "reference"):
+        # The reference's own published shapes (fp32, non-causal, Apple M1 Max figures in
+        # docs/ARCHITECTURE.md:910-912, :1184-1186, :1262-1264), run on the same kernels
+        # any fp32 caller reaches.
+        ref = {}
+        for n in (1024, 2048, 4096):
+            ms, variant = bench_gemm(core, ops, n, 2, args.sample_ms, element="f32")
+            ref[f"gemm_f32_{n}"] = {"tflops": round(gemm_flops(n, n, n) / (ms * 1e-3) / 1e12, 2),
+                                    "ms": round(ms, 4), "variant": variant}
+        for heads, seq in ((8, 512), (8, 1024), (16, 2048)):
+            _, kr = bench_attention(core, ops, 1, heads, seq, 64, False, 0, 2, args.sample_ms,
+                                    element="f32")
+            ms_f = kr["attn_fwd"]["ms"]
+            ms_b = sum(kr[k]["ms"] for k in ("attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv"))
+            ref[f"fa2_f32_h{heads}_s{seq}_d64"] = {
+                "fwd_tflops": round(attention_flops(heads, seq, 64, False) / (ms_f * 1e-3) / 1e12, 3),
+                "bwd_tflops": round(attention_flops(heads, seq, 64, False, backward=True)
+                                    / (ms_b * 1e-3) / 1e12, 3),
+                "fwd_ms": round(ms_f, 4), "bwd_ms": round(ms_b, 4)}
+        components["reference_shapes_f32"] = ref
     if args.only in ("all", "gemm"):
         n = 8192
         ms, variant = bench_gemm(core, ops, n, args.warmup, args.sample_ms)
