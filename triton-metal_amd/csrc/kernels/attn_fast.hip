@@ -13,10 +13,9 @@
  *     a reduction over the four 16-lane groups and the row sum none until the end;
  *   - O^T = V^T P^T keeps the lane <-> query ownership, so P goes from the
  *     softmax straight into the B operand and the rescale is lane-local;
- *   - K [64 keys][D] and V^T [D][64 keys] are double-buffered in LDS, K in
- *     16-byte chunks XOR-swizzled by row, V^T in 8-byte units XOR-swizzled by
- *     row pair, both conflict-free for the MFMA operand reads; V is transposed
- *     in registers on its way from HBM to LDS;
+ *   - K and V tiles [64 keys][D] are double-buffered in LDS in their natural
+ *     row order, 16-byte chunks XOR-swizzled by row; K feeds the A operand by
+ *     ds_read_b128, V^T by the transposing ds_read_b64_tr_b16;
  *   - causal: key blocks past the workgroup's last query are never visited,
  *     waves skip blocks entirely above their queries, masking only runs on
  *     blocks that straddle the diagonal or n_ctx;
@@ -66,9 +65,9 @@ TM_DEV int xcd_remap(int wg, int nwg) {
 typedef __attribute__((address_space(3))) void lds_void;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-TM_DEV void global_to_lds16(const void *src, char *lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void *)lds_wave_base, 16, 0, 0);
-}
+/* Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data format,
+ * no swizzle, no stride. */
+#define TM_BUFFER_WORD3 0x00020000
 
 /* Per-row statistics of one block of 32 queries, HBM -> LDS with the tiles:
  * wave 0 copies L[q0 .. q0+31] then Delta[q0 .. q0+31] (one 4-byte element per
@@ -105,21 +104,28 @@ TM_DEV int tile_off(int row, int chunk) {
 }
 
 /* Copy rows [k0, k0 + ROWS) of a [n, D] tensor (row stride ss elements) into an
- * LDS tile, the four waves sharing the work.  Rows at or past n are clamped to
- * row n-1: finite values that the caller masks (scores to -inf, P to 0). */
+ * LDS tile, the four waves sharing the work, by buffer_load ... lds through a
+ * buffer resource based at row k0: the lane offsets are loop-invariant, the
+ * per-block base is scalar arithmetic, and rows at or past n lie outside the
+ * resource, so the hardware delivers zeros for them (finite values that the
+ * caller masks: scores to -inf, P to 0).  The host only takes this path when a
+ * head's rows span fewer than 2^31 bytes. */
 template <typename T, int D, int ROWS>
 TM_DEV void stage_rows(const T *src, int64_t ss, int k0, int n, char *tile, int wave, int lane) {
   constexpr int CPR = D / 8;                      /* 16-byte chunks per row */
   constexpr int RPI = 64 / CPR;                   /* rows per wave instruction */
   constexpr int INSTR = ROWS / RPI / 4;           /* instructions per wave */
   static_assert(INSTR >= 1 && ROWS % (RPI * 4) == 0, "tile rows");
+  const int64_t bytes = (int64_t)(n - k0 - 1) * ss * 2 + D * 2;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(src + (int64_t)k0 * ss), 0, (int)min(bytes, (int64_t)INT32_MAX), TM_BUFFER_WORD3);
 #pragma unroll
   for (int i = 0; i < INSTR; ++i) {
     const int t = wave * INSTR + i;
     const int row = t * RPI + lane / CPR;
     const int chunk = (lane % CPR) ^ swz<D>(row);
-    const int key = min(k0 + row, n - 1);
-    global_to_lds16(src + (int64_t)key * ss + chunk * 8, tile + t * 1024);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(tile + t * 1024), 16,
+                                             (int)(row * ss * 2) + chunk * 16, 0, 0, 0);
   }
 }
 
@@ -161,7 +167,8 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   __shared__ __align__(1024) char lds_b[2 * TILE];
 
   typedef typename Vec8<T>::type v8;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); /* uniform: LDS bases are scalar */
   const int g = lane >> 4, c = lane & 15;
   const int n = p.n_ctx;
   const int nqb = (n + BM - 1) / BM;
@@ -241,11 +248,10 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
             s[kt][qt][r] = (key >= n || (CAUSAL && key > qi)) ? TM_NEG_INF : s[kt][qt][r];
           }
       }
-      float mx = s[0][qt][0];
+      float mx = vmax(s[0][qt][0], s[0][qt][1]);
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][qt][r]);
+      for (int e = 2; e < 16; e += 2)
+        mx = vmax(vmax(mx, s[e >> 2][qt][e & 3]), s[e >> 2][qt][(e & 3) + 1]);
       mxs[qt] = group4_max(mx) * qk_scale;
     }
     /* Lazy rescale: a row's exponent offset m only moves when the block max
@@ -267,15 +273,15 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
     }
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      float rs = 0.f;
       float pv[4][4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < 4; ++r)
           pv[kt][r] = fast_exp2(__builtin_fmaf(s[kt][qt][r], qk_scale, -m_i[qt]));
-          rs += pv[kt][r];
-        }
+      float rs = pv[0][0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) rs += pv[e >> 2][e & 3];
       l_i[qt] += rs;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
@@ -344,7 +350,8 @@ TM_DEV void attn_pre_fast(const TmAttnPreArgs &p) {
   constexpr int LPR = D / 8;        /* lanes per row */
   constexpr int RPI = 64 / LPR;     /* rows per wave instruction */
   constexpr int NI = 64 / RPI;      /* instructions per wave (64 rows) */
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); /* uniform: LDS bases are scalar */
   const int n = p.n_ctx;
   const int nrb = (n + 255) / 256;
   const int bh = blockIdx.x / nrb;
@@ -399,7 +406,8 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
   __shared__ __align__(1024) char lds_b[2 * TILE];
 
   typedef typename Vec8<T>::type v8;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); /* uniform: LDS bases are scalar */
   const int g = lane >> 4, c = lane & 15;
   const int n = p.n_ctx;
   const int nqb = (n + BM - 1) / BM;
@@ -565,7 +573,8 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
   __shared__ __align__(1024) char lds_2[BUF];
 
   typedef typename Vec8<T>::type v8;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); /* uniform: LDS bases are scalar */
   const int g = lane >> 4, c = lane & 15;
   const int n = p.n_ctx;
   const int nkb = (n + BN - 1) / BN;

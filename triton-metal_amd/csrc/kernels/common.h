@@ -79,15 +79,35 @@ enum GemmEpilogue { EPI_NONE = 0, EPI_BIAS_RELU = 1 };
 
 /* ---- wavefront reductions over the four 16-lane groups --------------------- */
 
+/* IEEE maximum (NaN-propagating); gfx950 has v_maximum3_f32 for it, so a
+ * chain of two needs one instruction and no canonicalising moves. */
+TM_DEV float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+/* x and x[lane ^ 32] (resp. 16) through the gfx950 row-swap moves
+ * v_permlane32_swap / v_permlane16_swap: no LDS round trip.  Swapping x with
+ * itself leaves lane i holding {x[i], x[i ^ 32]} in some order. */
+TM_DEV void swap32(float x, float &a, float &b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+TM_DEV void swap16(float x, float &a, float &b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
 TM_DEV float group4_max(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16, 64));
-  x = fmaxf(x, __shfl_xor(x, 32, 64));
-  return x;
+  float a, b;
+  swap32(x, a, b);
+  swap16(vmax(a, b), a, b);
+  return vmax(a, b);
 }
 TM_DEV float group4_sum(float x) {
-  x += __shfl_xor(x, 16, 64);
-  x += __shfl_xor(x, 32, 64);
-  return x;
+  float a, b;
+  swap32(x, a, b);
+  swap16(a + b, a, b);
+  return a + b;
 }
 
 TM_DEV float wave_sum(float x) {

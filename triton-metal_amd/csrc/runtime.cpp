@@ -504,11 +504,16 @@ bool fast_paths_enabled() {
 
 /* The specialised attention kernels need a 16-bit element type, head_dim 64
  * or 128, 16-byte aligned rows and a positive finite scale. */
+/* The fast kernels copy K/V/Q/dO tiles through a buffer resource based at a
+ * head's first row: a head's rows must span fewer than 2^31 bytes. */
 bool attn_fast_ok(const BuiltinSpec &spec, int32_t stride_head, int32_t stride_seq,
-                  float sm_scale) {
+                  int32_t n_ctx, float sm_scale) {
+  const int64_t head_bytes =
+      ((int64_t)(n_ctx > 0 ? n_ctx - 1 : 0) * stride_seq + spec.head_dim) * 2;
   return fast_paths_enabled() && spec.element != Element::F32 &&
          (spec.head_dim == 64 || spec.head_dim == 128) && stride_seq % 8 == 0 &&
-         stride_head % 8 == 0 && std::isfinite(sm_scale) && sm_scale > 0.f;
+         stride_head % 8 == 0 && std::isfinite(sm_scale) && sm_scale > 0.f &&
+         head_bytes <= INT32_MAX;
 }
 
 int padded_head_dim(int d) { return d <= 32 ? 32 : d <= 64 ? 64 : d <= 96 ? 96 : 128; }
@@ -662,7 +667,7 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         plan.empty = true;
         return plan;
       }
-      if (attn_fast_ok(spec, p.stride_head, p.stride_seq, p.sm_scale)) {
+      if (attn_fast_ok(spec, p.stride_head, p.stride_seq, p.n_ctx, p.sm_scale)) {
         plan.variant = format("tm_attn_fwd_fast_%s_d%d%s", el, spec.head_dim,
                               spec.causal ? "_causal" : "");
         plan.grid[0] = (unsigned)(cdiv(p.n_ctx, 128) * heads);
@@ -703,7 +708,7 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         plan.empty = true;
         return plan;
       }
-      if (attn_fast_ok(spec, p.stride_head, p.stride_seq, 1.f)) {
+      if (attn_fast_ok(spec, p.stride_head, p.stride_seq, p.n_ctx, 1.f)) {
         plan.variant = format("tm_attn_pre_fast_%s_d%d", el, spec.head_dim);
         plan.grid[0] = (unsigned)(cdiv(p.n_ctx, 256) * heads);
       } else {
@@ -740,7 +745,7 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         plan.empty = true;
         return plan;
       }
-      const bool fast = attn_fast_ok(spec, stride_head, stride_seq, sm_scale);
+      const bool fast = attn_fast_ok(spec, stride_head, stride_seq, n_ctx, sm_scale);
       if (fast) {
         plan.grid[0] = (unsigned)(cdiv(n_ctx, 128) * heads);
       } else {
