@@ -808,6 +808,16 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
   }
   (void)gx;
   plan.function = builtin_function(plan.variant);
+  /* the workgroup size the planner chose must be one the code object was
+   * compiled for (its launch bounds): a larger one would run the kernel
+   * outside the assumptions its register and LDS allocation rest on */
+  int limit = 0;
+  hip_check(hipFuncGetAttribute(&limit, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, plan.function),
+            "hipFuncGetAttribute");
+  if ((int)plan.block > limit)
+    throw TmError(format("internal error: '%s' planned with %u threads per workgroup, but the "
+                         "kernel is built for at most %d",
+                         plan.variant.c_str(), plan.block, limit));
   return plan;
 }
 
