@@ -55,19 +55,15 @@ TM_DEV int xcd_remap(int wg, int nwg) {
 
 
 /* ---- LDS staging ----------------------------------------------------------
- * K and V tiles are copied HBM -> LDS by global_load_lds_dwordx4, which writes
- * each lane's 16 bytes to (wave-uniform LDS base) + 16 * lane: one instruction
- * fills 1 KB.  Rows keep their natural [key][d] order; the 16-byte chunk c of
+ * K and V tiles are copied HBM -> LDS by buffer_load_dwordx4 ... lds, which
+ * writes each lane's 16 bytes to (wave-uniform LDS base) + 16 * lane: one
+ * instruction fills 1 KB.  Rows keep their natural [key][d] order; the 16-byte chunk c of
  * row r is stored at chunk position c ^ (r & 7), so the 16-row MFMA operand
  * reads (K: 16 bytes per lane; V: ds_read_b64_tr_b16, 8 bytes per lane) spread
  * over all banks. */
 
-typedef __attribute__((address_space(3))) void lds_void;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-/* Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data format,
- * no swizzle, no stride. */
-#define TM_BUFFER_WORD3 0x00020000
 
 /* Per-row statistics of one block of BM queries, HBM -> LDS with the tiles:
  * wave w < BM/32 copies L[q0 + 32w .. +31] then Delta[q0 + 32w .. +31] to
@@ -80,7 +76,7 @@ TM_DEV void stage_stats(const float *L, const float *Dl, int q0, int n, char *ld
   if (wave >= BM / 32) return;
   const int q = min(q0 + wave * 32 + (lane & 31), n - 1);
   const float *src = lane < 32 ? L + q : Dl + q;
-  __builtin_amdgcn_global_load_lds(src, (lds_void *)(lds + wave * 256), 4, 0, 0);
+  lds_copy4_global(src, lds_addr(lds + wave * 256));
 }
 
 /* wait for this wave's outstanding vector-memory operations (vmcnt = 0) */
@@ -119,15 +115,13 @@ TM_DEV void stage_rows(const T *src, int64_t ss, int k0, int n, char *tile, int 
   constexpr int INSTR = ROWS / RPI / 4;           /* instructions per wave */
   static_assert(INSTR >= 1 && ROWS % (RPI * 4) == 0, "tile rows");
   const int64_t bytes = (int64_t)(n - k0 - 1) * ss * 2 + D * 2;
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(src + (int64_t)k0 * ss), 0, (int)min(bytes, (int64_t)INT32_MAX), TM_BUFFER_WORD3);
+  const u32x4 rs = raw_buffer_rsrc(src + (int64_t)k0 * ss, bytes);
 #pragma unroll
   for (int i = 0; i < INSTR; ++i) {
     const int t = wave * INSTR + i;
     const int row = t * RPI + lane / CPR;
     const int chunk = (lane % CPR) ^ swz<D>(row);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(tile + t * 1024), 16,
-                                             (int)(row * ss * 2) + chunk * 16, 0, 0, 0);
+    lds_copy16_buffer(rs, (int)(row * ss * 2) + chunk * 16, lds_addr(tile + t * 1024));
   }
 }
 

@@ -115,6 +115,49 @@ TM_DEV float wave_sum(float x) {
   return x;
 }
 
+/* ---- HBM -> LDS copies ------------------------------------------------------
+ * buffer_load ... lds / global_load_lds write each lane's bytes to LDS at
+ * M0 + 4-byte or 16-byte lane slots, without passing through registers.  They
+ * are issued from inline assembly on purpose: the compiler models an
+ * in-flight LDS copy as an unordered LGKM event and then waits lgkmcnt(0) for
+ * every LDS read issued while a copy is outstanding, which serialises the
+ * operand reads of the whole step.  On gfx950 the copy is counted by vmcnt
+ * only (a probe reads LDS 108 cycles after issuing a copy that lands 1800
+ * cycles later), so the reads can be pipelined.  The compiler does not see
+ * these writes: every caller waits for its copies itself (s_waitcnt
+ * vmcnt(0)) and then barriers before any wave reads the tile.  The "memory"
+ * clobber keeps the compiler's own LDS accesses on their side of the copy. */
+
+/* lane slot = 16 bytes at M0 + 16 * lane, from the raw buffer described by
+ * the (wave-uniform) resource `rsrc` at byte offset `voffset` */
+TM_DEV void lds_copy16_buffer(u32x4 rsrc, int voffset, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(lds_base), "v"(voffset), "s"(rsrc) : "memory", "m0");
+}
+/* lane slot = 16 bytes at M0 + 16 * lane, from `src` */
+TM_DEV void lds_copy16_global(const void *src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(lds_base), "v"(src) : "memory", "m0");
+}
+/* lane slot = 4 bytes at M0 + 4 * lane, from `src` */
+TM_DEV void lds_copy4_global(const void *src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               :: "s"(lds_base), "v"(src) : "memory", "m0");
+}
+/* LDS byte address of a shared-memory pointer, made wave-uniform (M0 source) */
+TM_DEV uint32_t lds_addr(const void *p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)p);
+}
+/* A raw buffer resource (gfx9 family: 48-bit base, stride 0, `bytes` records,
+ * 32-bit data format) for the wave-uniform base `p`. */
+TM_DEV u32x4 raw_buffer_rsrc(const void *p, int64_t bytes) {
+  const uint64_t a = (uint64_t)p;
+  const int32_t n = (int32_t)(bytes < (int64_t)INT32_MAX ? bytes : (int64_t)INT32_MAX);
+  return (u32x4){(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a),
+                 (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xffffu,
+                 (uint32_t)__builtin_amdgcn_readfirstlane(n), 0x00020000u};
+}
+
 /* log2(e), written out: the reference folds sm_scale into the exp2 domain with
  * this constant (Sources/TritonMetalBench/AttentionKernel.swift:79-80). */
 #define TM_LOG2E 1.44269504088896340736f

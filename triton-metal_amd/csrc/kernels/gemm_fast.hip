@@ -9,7 +9,8 @@
  * of C; each wave a 128 x 64 sub-tile on v_mfma_f32_16x16x32_{bf16,f16}
  * (8 x 4 accumulators of 16 x 16).  Per K step of 64:
  *   - A [256 x 64] and B [64 x 256] tiles are copied HBM -> LDS with
- *     global_load_lds_dwordx4 in their natural row-major layouts (double
+ *     global_load_lds_dwordx4 (issued from inline assembly, so the compiler
+ *     pipelines the operand reads behind it) in their natural row-major layouts (double
  *     buffered, 128 KB of LDS), 16-byte chunks XOR-swizzled by row;
  *   - the A operand (row m, 8 consecutive k) is one ds_read_b128;
  *   - the B operand (column n, 8 consecutive k) is two ds_read_b64_tr_b16:
@@ -29,10 +30,9 @@ template <> struct GVec8<bf16_t> { typedef bf16x8 type; };
 template <> struct GVec8<f16_t> { typedef f16x8 type; };
 
 typedef short gs16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void glds_void;
 
 TM_DEV void g_global_to_lds16(const void *src, char *lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(src, (glds_void *)lds_wave_base, 16, 0, 0);
+  lds_copy16_global(src, lds_addr(lds_wave_base));
 }
 TM_DEV void g_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
