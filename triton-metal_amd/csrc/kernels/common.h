@@ -10,8 +10,10 @@
  *   v_mfma_f32_32x32x16_bf16  A: row l%32, k = 8h .. 8h+7 B: col l%32, k = 8h .. 8h+7
  *   (and _f16, h = l / 32)    D: col l%32, rows 8j + 4h .. 8j + 4h + 3 in
  *                                floats 4j .. 4j+3 (j = 0..3; 16 floats)
- * On gfx950 the 32x32x16 form sustains close to the dense peak back to back;
- * the 16x16x32 form issues at about four fifths of it.
+ * On gfx950 both forms reach the dense peak when enough independent
+ * accumulators are in flight (two waves per SIMD, or eight chains in one
+ * wave: about 17 cycles per 16x16x32, 34 per 32x32x16); with four chains in a
+ * single wave the 16x16x32 form is latency-bound at about 19 cycles.
  * The contraction index k may be permuted freely as long as A and B use the
  * same permutation; the attention kernels rely on that to feed the softmax
  * output (rows 4g..4g+3 of a 16-row tile) straight back in as a B operand.
