@@ -175,3 +175,47 @@ def test_unaligned_gemm_takes_the_generic_kernel(m, n, k, device):
     c, want, variant = _gemm(m, n, k, "bf16")
     assert variant == "tm_gemm_generic_bf16"
     assert T.hybrid_error(c, want) <= 2e-2
+
+
+@pytest.mark.parametrize("seq,expect", [(1024, "fast"), (1025, "generic")])
+def test_head_span_at_the_buffer_resource_limit(seq, expect, device):
+    """The fast kernels copy tiles through a buffer resource based at a head's
+    first row, so a head whose rows span 2^31 bytes or more takes the generic
+    kernel.  Rows 2 MiB apart put the boundary between 1024 rows (2^31 - 2 MiB
+    + 128 bytes: fast, with 32-bit lane offsets up to 2^31 - 2 MiB) and 1025
+    rows (2^31 + 128 bytes: generic).  Only the rows themselves are written and
+    read back; the buffers (about 2 GiB each) are never touched elsewhere."""
+    from triton_metal.buffer import bf16_bits, bf16_values
+    dim, ss = 64, 1 << 20
+    extent = (seq - 1) * ss + dim
+    rng = np.random.default_rng(7)
+    dense = [round_to(rng.standard_normal((1, seq, dim), dtype=np.float32), "bf16")
+             for _ in range(3)]
+    handles = [_core.alloc_buffer(extent * 2) for _ in range(4)]
+    lse = DeviceBuffer((1, seq), "float32")
+    try:
+        for handle, x in zip(handles, dense):
+            bits = bf16_bits(x[0])
+            for i in range(seq):
+                row = np.ascontiguousarray(bits[i])
+                _core.buffer_write(handle, i * ss * 2, row.ctypes.data, dim * 2)
+        kern = ops.library("bf16", dim, False).kernels["attn_fwd"]
+        B, I, F = _core.ARG_BUFFER, _core.ARG_I32, _core.ARG_F32
+        _core.launch(kern, (1, 1, 1), 128, [B, B, B, B, F, I, I, I, B, I],
+                     handles + [_core.float_bits(1 / math.sqrt(dim)), seq * ss, ss, seq,
+                                lse.tm_handle, seq])
+        variant = _core.kernel_variant(kern)
+        o_bits = np.zeros((seq, dim), np.uint16)
+        for i in range(seq):
+            _core.buffer_read(handles[3], i * ss * 2, o_bits[i].ctypes.data, dim * 2)
+        o = bf16_values(o_bits)[None]
+        lse_got = lse.float32()
+    finally:
+        for handle in handles:
+            _core.free_buffer(handle)
+        lse.free()
+    assert f"_{expect}_" in variant, variant
+    q, k, v = dense
+    o_want, _, lse_want = R.attention_forward(q, k, v, 1 / math.sqrt(dim), False)
+    assert T.max_abs_error(o, o_want) <= 2e-2
+    assert T.max_abs_error(lse_got, lse_want) <= 2e-3
