@@ -146,9 +146,11 @@ TM_DEV void lds_copy4_global(const void *src, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
                :: "s"(lds_base), "v"(src) : "memory", "m0");
 }
-/* LDS byte address of a shared-memory pointer, made wave-uniform (M0 source) */
+/* LDS byte address of a shared-memory pointer (address-space cast, not the
+ * flat aperture address), made wave-uniform: the M0 operand of the copies */
 TM_DEV uint32_t lds_addr(const void *p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)p);
+  typedef __attribute__((address_space(3))) const char lds_char;
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_char *)p);
 }
 /* A raw buffer resource (gfx9 family: 48-bit base, stride 0, `bytes` records,
  * 32-bit data format) for the wave-uniform base `p`. */
