@@ -17,8 +17,9 @@
  *     row order, 16-byte chunks XOR-swizzled by row; K feeds the A operand by
  *     ds_read_b128, V^T by the transposing ds_read_b64_tr_b16;
  *   - causal: key blocks past the workgroup's last query are never visited,
- *     waves skip blocks entirely above their queries, masking only runs on
- *     blocks that straddle the diagonal or n_ctx;
+ *     masking only runs on blocks that straddle the diagonal or n_ctx (a wave
+ *     whose queries all lie below a block computes it fully masked: skipping
+ *     it measured no faster, since the wave then waits at the barrier);
  *   - the 1-D grid is remapped so that each XCD (workgroups are dealt to the
  *     8 XCDs round-robin) runs a contiguous range of heads, keeping one head's
  *     K and V in that XCD's L2; within a head, causal blocks run heaviest first.
