@@ -128,23 +128,28 @@ TM_DEV float wave_sum(float x) {
  * cycles later), so the reads can be pipelined.  The compiler does not see
  * these writes: every caller waits for its copies itself (s_waitcnt
  * vmcnt(0)) and then barriers before any wave reads the tile.  The "memory"
- * clobber keeps the compiler's own LDS accesses on their side of the copy. */
+ * clobber keeps the compiler's own LDS accesses on their side of the copy.
+ * M0 (the LDS base) is an operand bound to the register itself, so the
+ * compiler knows it is set.  The compiler's hazard recognizer does not look
+ * inside the asm, so the asm opens with the wait states its operands may
+ * need: 5 after a VALU write of an SGPR the copy reads (the resource words
+ * come from v_readfirstlane), which also covers the 1 after a write of M0. */
 
 /* lane slot = 16 bytes at M0 + 16 * lane, from the raw buffer described by
  * the (wave-uniform) resource `rsrc` at byte offset `voffset` */
 TM_DEV void lds_copy16_buffer(u32x4 rsrc, int voffset, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :: "s"(lds_base), "v"(voffset), "s"(rsrc) : "memory", "m0");
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "{m0}"(lds_base), "v"(voffset), "s"(rsrc) : "memory");
 }
 /* lane slot = 16 bytes at M0 + 16 * lane, from `src` */
 TM_DEV void lds_copy16_global(const void *src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :: "s"(lds_base), "v"(src) : "memory", "m0");
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "{m0}"(lds_base), "v"(src) : "memory");
 }
 /* lane slot = 4 bytes at M0 + 4 * lane, from `src` */
 TM_DEV void lds_copy4_global(const void *src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
-               :: "s"(lds_base), "v"(src) : "memory", "m0");
+  asm volatile("s_nop 4\n\tglobal_load_lds_dword %1, off"
+               :: "{m0}"(lds_base), "v"(src) : "memory");
 }
 /* LDS byte address of a shared-memory pointer (address-space cast, not the
  * flat aperture address), made wave-uniform: the M0 operand of the copies */
