@@ -14,8 +14,9 @@
  *   - O^T = V^T P^T keeps the lane <-> query ownership, so P goes from the
  *     softmax straight into the B operand and the rescale is lane-local;
  *   - K and V tiles [64 keys][D] are double-buffered in LDS in their natural
- *     row order, 16-byte chunks XOR-swizzled by row; K feeds the A operand by
- *     ds_read_b128, V^T by the transposing ds_read_b64_tr_b16;
+ *     row order, 16-byte chunks XOR-swizzled by row, each tile with the key
+ *     that suits its reads; K feeds the A operand by ds_read_b128, V^T by the
+ *     transposing ds_read_b64_tr_b16;
  *   - causal: key blocks past the workgroup's last query are never visited,
  *     masking only runs on blocks that straddle the diagonal or n_ctx (a wave
  *     whose queries all lie below a block computes it fully masked: skipping
@@ -83,23 +84,35 @@ TM_DEV void stage_stats(const float *L, const float *Dl, int q0, int n, char *ld
 /* wait for this wave's outstanding vector-memory operations (vmcnt = 0) */
 TM_DEV void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-/* 16-byte chunk position of logical chunk `chunk` in row `row`.  The XOR key
- * makes both operand read patterns conflict-free: 16 consecutive rows at one
- * chunk (ds_read_b128) and 8 consecutive rows at a chunk pair
- * (ds_read_b64_tr_b16).  D = 128: rows are 256 bytes, the key spreads 16 rows
- * over the 16 chunk positions with even keys for rows 0-7 of each group of 16;
- * D = 64: rows are 128 bytes, row parity picks the half, the key spreads each
- * parity class the same way. */
-template <int D>
+/* 16-byte chunk position of logical chunk `chunk` in row `row`: the chunk
+ * XORed with a key of the row.  Two read patterns meet the tiles: 16
+ * consecutive rows at one chunk (ds_read_b128) and 8 consecutive rows at a
+ * chunk pair (ds_read_b64_tr_b16).  No key serves both without conflicts.
+ * KEY_TR keeps the transposed reads conflict-free (D = 128: rows are 256
+ * bytes, the key spreads 16 rows over the 16 chunk positions with even keys
+ * for rows 0-7 of each group of 16; D = 64: rows are 128 bytes, row parity
+ * picks the half, the key spreads each parity class the same way); tiles read
+ * both ways keep it, as keys with fewer b128 conflicts measured slower there.
+ * KEY_B128 serves tiles read only by ds_read_b128. */
+enum SwizzleKey {
+  KEY_TR = 0,   /* tiles read both ways, or by the transposing reads only */
+  KEY_B128 = 1  /* tiles read only by ds_read_b128 of 16 consecutive rows */
+};
+
+template <int D, int KEY = KEY_TR>
 TM_DEV int swz(int row) {
+  /* row & 15 (D = 128) and row & 7 (D = 64) leave the 16-row ds_read_b128
+   * pattern with no bank conflicts (SQ_LDS_BANK_CONFLICT reads 0; the shared
+   * key conflicts on a third of the forward's LDS cycles) */
+  if (KEY == KEY_B128) return D == 128 ? (row & 15) : (row & 7);
   if (D == 128) return ((row & 7) << 1) | ((row >> 3) & 1);
   const int t = row >> 1;
   return ((t & 3) << 1) | ((t >> 2) & 1);
 }
 
-template <int D>
+template <int D, int KEY = KEY_TR>
 TM_DEV int tile_off(int row, int chunk) {
-  return row * (D * 2) + ((chunk ^ swz<D>(row)) << 4);
+  return row * (D * 2) + ((chunk ^ swz<D, KEY>(row)) << 4);
 }
 
 /* Copy rows [k0, k0 + ROWS) of a [n, D] tensor (row stride ss elements) into an
@@ -109,7 +122,7 @@ TM_DEV int tile_off(int row, int chunk) {
  * resource, so the hardware delivers zeros for them (finite values that the
  * caller masks: scores to -inf, P to 0).  The host only takes this path when a
  * head's rows span fewer than 2^31 bytes. */
-template <typename T, int D, int ROWS>
+template <typename T, int D, int ROWS, int KEY = KEY_TR>
 TM_DEV void stage_rows(const T *src, int64_t ss, int k0, int n, char *tile, int wave, int lane) {
   constexpr int CPR = D / 8;                      /* 16-byte chunks per row */
   constexpr int RPI = 64 / CPR;                   /* rows per wave instruction */
@@ -121,7 +134,7 @@ TM_DEV void stage_rows(const T *src, int64_t ss, int k0, int n, char *tile, int 
   for (int i = 0; i < INSTR; ++i) {
     const int t = wave * INSTR + i;
     const int row = t * RPI + lane / CPR;
-    const int chunk = (lane % CPR) ^ swz<D>(row);
+    const int chunk = (lane % CPR) ^ swz<D, KEY>(row);
     lds_copy16_buffer(rs, (int)(row * ss * 2) + chunk * 16, lds_addr(tile + t * 1024));
   }
 }
@@ -185,7 +198,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   const int kend = CAUSAL ? min(n, q0 + BM) : n;
   const int nblocks = (kend + BN - 1) / BN;
   if (nblocks > 0) {
-    stage_rows<T, D, BN>(Kg, ss, 0, n, lds_a, wave, lane);
+    stage_rows<T, D, BN, KEY_B128>(Kg, ss, 0, n, lds_a, wave, lane);
     stage_rows<T, D, BN>(Vg, ss, 0, n, lds_a + TILE, wave, lane);
   }
 
@@ -216,7 +229,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
     constexpr bool EDGE = decltype(edge_tag)::value;
     const int k0 = j * BN;
     if (j + 1 < nblocks) {
-      stage_rows<T, D, BN>(Kg, ss, k0 + BN, n, nxt, wave, lane);
+      stage_rows<T, D, BN, KEY_B128>(Kg, ss, k0 + BN, n, nxt, wave, lane);
       stage_rows<T, D, BN>(Vg, ss, k0 + BN, n, nxt + TILE, wave, lane);
     }
     /* S^T = K Q^T: 4 key tiles x 2 query tiles */
@@ -226,7 +239,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
       s[kt][0] = s[kt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const v8 a = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D>(kt * 16 + c, ks * 4 + g)));
+        const v8 a = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D, KEY_B128>(kt * 16 + c, ks * 4 + g)));
         s[kt][0] = mfma_16x16x32(a, as_vec8<T>(qf[0][ks]), s[kt][0]);
         s[kt][1] = mfma_16x16x32(a, as_vec8<T>(qf[1][ks]), s[kt][1]);
       }
