@@ -324,14 +324,16 @@ def _head_backward64(q, k, v, d_out, scale):
     return o, lse_nat, ds @ k * scale, ds.T @ q * scale, dv
 
 
-def test_config5_bf16_causal_forward_backward_full_size(device):
-    """B4 H32 S4096 D128 bf16 causal, N(0,1), scale 1/sqrt(128): O, LSE, dQ, dK,
-    dV.  Three heads against fp64 (2e-2 absolute on O and LSE, 2e-2 hybrid on
+@pytest.mark.parametrize("element", ["bf16", "f16"])
+def test_config5_causal_forward_backward_full_size(device, element):
+    """B4 H32 S4096 D128 causal in bf16 (the benchmark's element type) and f16
+    (the reference's own attention element type), N(0,1), scale 1/sqrt(128): O,
+    LSE, dQ, dK, dV.  Three heads against fp64 (2e-2 absolute on O and LSE, 2e-2 hybrid on
     the gradients); every head through size-independent identities of causal
     attention: O[0] = V[0], dQ[0] = 0, sum_j dK_j = 0, sum_j dV_j = sum_i dO_i."""
     bh, seq, dim = 128, 4096, 128
-    q, k, v, d_out = normal_inputs(bh, seq, dim, "bf16", seed=5)
-    r = Runner(bh, seq, dim, "bf16", causal=True)
+    q, k, v, d_out = normal_inputs(bh, seq, dim, element, seed=5)
+    r = Runner(bh, seq, dim, element, causal=True)
     try:
         o, lse = r.forward(q, k, v)
         r.layer.upload("do", d_out)
