@@ -749,10 +749,15 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
   if (nblocks > 0) {
     stage(lds_0, 0);
     if (nblocks > 1) stage(lds_1, 1);
-    wait_vmem();
-    __syncthreads();
-    scores(Edge{}, lds_0, 0, pf, dsf);
   }
+  /* Unconditional: the compiler then knows the K/V fragment loads are complete
+   * on every path into the step loop.  Left inside the branch, its wait-count
+   * pass kept them pending at the loop header and waited vmcnt(N) inside every
+   * step, where the hardware count also holds the step's own tile copies (which
+   * the compiler does not see), so the waits stalled on those copies. */
+  wait_vmem();
+  __syncthreads();
+  if (nblocks > 0) scores(Edge{}, lds_0, 0, pf, dsf);
 
   /* Block b is masked if it lies in the diagonal band (b < band) or runs past
    * n (b >= full).  Step i masks the softmax of block i+1. */
