@@ -134,15 +134,22 @@ def test_variant_selection(element, dim, stride_seq, expect, device):
     _check(out, dense, dim, False, tol=2e-2 if element != "f32" else 1e-4)
 
 
-def _gemm(m, n, k, element, lda=None, ldb=None, ldc=None, seed=0):
+def _gemm(m, n, k, element, lda=None, ldb=None, ldc=None, seed=0, poison=False, extra_rows=0):
+    """C = A B with leading dimensions lda/ldb/ldc.  `poison` fills the padding
+    columns of A (k..lda) with inf and of B (n..ldb) with NaN: a kernel that
+    lets them reach a stored output element fails.  C gets `extra_rows` rows
+    past row m, preset to -7 like its padding columns."""
     lda, ldb, ldc = lda or k, ldb or n, ldc or n
     rng = np.random.default_rng(seed)
     a = round_to(rng.standard_normal((m, lda), dtype=np.float32), element)
     b = round_to(rng.standard_normal((k, ldb), dtype=np.float32), element)
+    if poison:
+        a[:, k:] = np.inf
+        b[:, n:] = np.nan
     dtype = DT[element]
     A = DeviceBuffer.from_numpy(a, dtype)
     B = DeviceBuffer.from_numpy(b, dtype)
-    C = DeviceBuffer.from_numpy(np.full((m, ldc), -7.0, np.float32), dtype)
+    C = DeviceBuffer.from_numpy(np.full((m + extra_rows, ldc), -7.0, np.float32), dtype)
     kern = ops.library(element).kernels["matmul_kernel"]
     try:
         grid, kinds, values = ops.matmul_args(A, B, C, m, n, k, (lda, 1, ldb, 1, ldc, 1))
@@ -170,11 +177,37 @@ def test_fast_gemm_shapes_and_strides(element, m, n, k, lda, ldb, ldc, device):
         assert np.all(c[:, n:] == -7.0)
 
 
-@pytest.mark.parametrize("m,n,k", [(255, 256, 64), (256, 256, 60), (300, 200, 100)])
-def test_unaligned_gemm_takes_the_generic_kernel(m, n, k, device):
-    c, want, variant = _gemm(m, n, k, "bf16")
-    assert variant == "tm_gemm_generic_bf16"
-    assert T.hybrid_error(c, want) <= 2e-2
+@pytest.mark.parametrize("element", ["bf16", "f16"])
+@pytest.mark.parametrize("m,n,k,lda,ldb,ldc", [
+    (255, 256, 64, None, None, None),    # M short of a tile
+    (256, 264, 64, None, None, None),    # N one chunk past a tile
+    (256, 256, 72, None, None, None),    # K past the last whole k-step
+    (129, 257, 65, 72, 264, 260),        # the reference's ragged shape (DotTests), padded rows
+    (1, 1, 1, 8, 8, 4),                  # one element
+    (300, 1000, 136, None, None, None),
+    (513, 777, 1000, 1000, 784, 780),
+])
+def test_ragged_gemm(element, m, n, k, lda, ldb, ldc, device):
+    """Any M, N, K with 16-byte aligned rows of A and B run the ragged
+    specialised kernel: masked to the matrix, with inf/NaN in the operands'
+    padding and sentinel rows and columns around C."""
+    c, want, variant = _gemm(m, n, k, element, lda, ldb, ldc, poison=True, extra_rows=3)
+    assert variant == f"tm_gemm_ragged_{element}"
+    assert np.all(np.isfinite(c[:m, :n]))
+    assert T.hybrid_error(c[:m, :n], want) <= 2e-2
+    assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)
+
+
+@pytest.mark.parametrize("m,n,k,lda,ldb,variant", [
+    (256, 256, 60, None, None, "generic"),    # rows of A not 16-byte aligned
+    (300, 200, 100, None, None, "generic"),
+    (255, 256, 64, None, None, "ragged"),
+    (512, 256, 128, None, None, "fast"),
+])
+def test_gemm_kernel_choice(m, n, k, lda, ldb, variant, device):
+    c, want, got = _gemm(m, n, k, "bf16", lda, ldb)
+    assert got == f"tm_gemm_{variant}_bf16"
+    assert T.hybrid_error(c[:, :n], want) <= 2e-2
 
 
 @pytest.mark.parametrize("seq,expect", [(1024, "fast"), (1025, "generic")])

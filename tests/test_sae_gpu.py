@@ -111,7 +111,9 @@ def test_short_buffers_are_refused(device):
 @pytest.mark.parametrize("element", ["bf16", "f16"])
 @pytest.mark.parametrize("rows,model,features,variant", [
     (512, 1024, 2048, "fast"),      # whole 256 x 256 x 64 tiles
-    (100, 300, 700, "generic"),     # ragged
+    (100, 300, 700, "generic"),     # rows not 16-byte aligned
+    (100, 512, 1000, "ragged"),     # M and N short of whole tiles
+    (333, 136, 264, "ragged"),      # ragged K
 ])
 def test_16bit_matches_the_oracle(device, element, rows, model, features, variant):
     rng = np.random.default_rng(5)

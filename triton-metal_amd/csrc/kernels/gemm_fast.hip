@@ -1,17 +1,21 @@
 /*
  * Specialised gfx950 GEMM for 16-bit element types: C = A @ B with A [M, K],
- * B [K, N], C [M, N] row-major (unit inner stride, 16-byte aligned rows),
- * M and N multiples of 256, K a multiple of 64; f32 accumulation, output
- * rounded to the element type (the reference's matmul_kernel semantics,
- * Sources/TritonMetalBench/GEMMKernel.swift:28-174).
+ * B [K, N], C [M, N] row-major (unit inner stride, 16-byte aligned rows of A
+ * and B, lda >= K, ldb >= N); f32 accumulation, output rounded to the element
+ * type (the reference's matmul_kernel semantics,
+ * Sources/TritonMetalBench/GEMMKernel.swift:28-174).  Two instantiations:
+ * the aligned one for M and N multiples of 256 and K a multiple of 64, and
+ * the ragged one for any other M, N, K, which masks its last k-step and its
+ * stores.
  *
  * Tiling: one 512-thread workgroup (8 waves, 2 x 4) computes a 256 x 256 tile
  * of C; each wave a 128 x 64 sub-tile on v_mfma_f32_16x16x32_{bf16,f16}
  * (8 x 4 accumulators of 16 x 16).  Per K step of 64:
  *   - A [256 x 64] and B [64 x 256] tiles are copied HBM -> LDS with
- *     global_load_lds_dwordx4 (issued from inline assembly, so the compiler
- *     pipelines the operand reads behind it) in their natural row-major layouts (double
- *     buffered, 128 KB of LDS), 16-byte chunks XOR-swizzled by row;
+ *     buffer_load ... lds (issued from inline assembly, so the compiler
+ *     pipelines the operand reads behind it) in their natural row-major
+ *     layouts (double buffered, 128 KB of LDS), 16-byte chunks XOR-swizzled
+ *     by row; the buffer range check turns rows past the matrix into zeros;
  *   - the A operand (row m, 8 consecutive k) is one ds_read_b128;
  *   - the B operand (column n, 8 consecutive k) is two ds_read_b64_tr_b16:
  *     lane i of a 16-lane group receives element (i & 3) of the 8 bytes
@@ -19,6 +23,11 @@
  *     columns n0 + 4q .. +3;
  *   - the MFMA takes B as its first operand, producing C^T tiles: each lane
  *     then holds 4 consecutive columns of one row, stored as one 8-byte write.
+ * Ragged K: the last step's A fragments are zeroed past column K in
+ * registers (the copies there read the next row, or the 16-byte rounding of
+ * the last one), and B's rows past K arrive as zeros, so no value from outside
+ * the matrices reaches a stored element.  Columns of B past N and rows of A
+ * past M feed only the outputs past N and M, which are not stored.
  * The 1-D grid is remapped so each XCD owns a contiguous range of tiles,
  * walked in groups of 8 tile rows so concurrently running tiles share A and B
  * panels in that XCD's L2.
@@ -31,9 +40,6 @@ template <> struct GVec8<f16_t> { typedef f16x8 type; };
 
 typedef short gs16x4 __attribute__((ext_vector_type(4)));
 
-TM_DEV void g_global_to_lds16(const void *src, char *lds_wave_base) {
-  lds_copy16_global(src, lds_addr(lds_wave_base));
-}
 TM_DEV void g_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 TM_DEV int g_xcd_remap(int wg, int nwg) {
@@ -59,28 +65,88 @@ TM_DEV int a_off(int row, int chunk) { return row * 128 + ((chunk ^ a_swz(row)) 
 TM_DEV int b_swz(int row) { return ((row & 3) | ((row >> 1) & 4)) << 1; }
 TM_DEV int b_off(int row, int chunk) { return row * 512 + ((chunk ^ b_swz(row)) << 4); }
 
+/* Each copy instruction moves a few whole rows of a tile through a buffer
+ * resource based at its first row, whose range ends at the matrix's last
+ * element (rounded up to 16 bytes, inside the allocation's 256-byte padding):
+ * rows past the last row of A or B are read as zeros, and a lane's byte
+ * offset is the same for every instruction and k-step, so the addresses cost
+ * only scalar instructions.  `rows_left` counts the valid rows from `base`,
+ * `width` the valid elements of a row. */
+template <int ROWS>
+TM_DEV void copy_rows(const void *base, int rows_left, int64_t ld, int width, int voff, char *slot) {
+  const int rows = min(rows_left, ROWS);
+  const int64_t bytes = rows > 0 ? ((int64_t)(rows - 1) * ld + ((width + 7) & ~7)) * 2 : 0;
+  lds_copy16_buffer(raw_buffer_rsrc(base, bytes), voff, lds_addr(slot));
+}
+
+/* A [256 x 64] tile, k0 = 0 at `a`: 32 instructions of 8 rows (4 per wave);
+ * lane l copies row 8t + (l >> 3), source chunk (l & 7) ^ a_swz(row). */
 template <typename T>
-TM_DEV void stage_a(const T *A, int64_t lda, int m0, int k0, char *tile, int wave, int lane) {
-  /* 32 instructions of 8 rows each, 4 per wave */
+TM_DEV void stage_a(const T *a, int64_t lda, int rows_left, int width, int voff, char *tile, int wave) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = wave * 4 + i;
+    copy_rows<8>(a + (int64_t)(t * 8) * lda, rows_left - t * 8, lda, width, voff, tile + t * 1024);
+  }
+}
+TM_DEV int a_lane_offset(int64_t lda, int lane) {
+  const int r = lane >> 3; /* a_swz(8t + r) = a_swz(r) */
+  return r * (int)lda * 2 + (((lane & 7) ^ a_swz(r)) << 4);
+}
+
+/* B [64 x 256] tile: 32 instructions of 2 rows (4 per wave); lane l copies
+ * row 2t + (l >> 5), source chunk (l & 31) ^ b_swz(row).  For t = 4w + i,
+ * b_swz(row) depends on the lane, w and i & 1 only. */
+template <typename T>
+TM_DEV void stage_b(const T *b, int64_t ldb, int rows_left, int width, const int (&voff)[2], char *tile,
+                    int wave) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = wave * 4 + i;
+    copy_rows<2>(b + (int64_t)(t * 2) * ldb, rows_left - t * 2, ldb, width, voff[i & 1], tile + t * 1024);
+  }
+}
+TM_DEV void b_lane_offsets(int64_t ldb, int wave, int lane, int (&voff)[2]) {
+  const int h = lane >> 5;
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+    voff[e] = h * (int)ldb * 2 + (((lane & 31) ^ b_swz(wave * 8 + 2 * e + h)) << 4);
+}
+
+/* The aligned kernel's copies: every row and column of a tile is inside the
+ * matrix, and plain global addresses measured 1.5-3% faster at 8192^3 than
+ * the buffer-resource copies above (the same tiles, the same LDS layout). */
+TM_DEV void global_rows_to_lds(const void *src, char *slot) { lds_copy16_global(src, lds_addr(slot)); }
+
+template <typename T>
+TM_DEV void stage_a_global(const T *a, int64_t lda, int k0, char *tile, int wave, int lane) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = wave * 4 + i;
     const int row = t * 8 + (lane >> 3);
     const int chunk = (lane & 7) ^ a_swz(row);
-    g_global_to_lds16(A + (int64_t)(m0 + row) * lda + k0 + chunk * 8, tile + t * 1024);
+    global_rows_to_lds(a + (int64_t)row * lda + k0 + chunk * 8, tile + t * 1024);
   }
 }
 
 template <typename T>
-TM_DEV void stage_b(const T *B, int64_t ldb, int k0, int n0, char *tile, int wave, int lane) {
-  /* 32 instructions of 2 rows each, 4 per wave */
+TM_DEV void stage_b_global(const T *b, int64_t ldb, int k0, char *tile, int wave, int lane) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = wave * 4 + i;
     const int row = t * 2 + (lane >> 5);
     const int chunk = (lane & 31) ^ b_swz(row);
-    g_global_to_lds16(B + (int64_t)(k0 + row) * ldb + n0 + chunk * 8, tile + t * 1024);
+    global_rows_to_lds(b + (int64_t)(k0 + row) * ldb + chunk * 8, tile + t * 1024);
   }
+}
+
+/* Keep the first `valid` 16-bit elements of an operand fragment, zero the
+ * rest (the k columns past K in the last k-step of a ragged GEMM). */
+TM_DEV u32x4 keep_first(u32x4 v, int valid) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w)
+    v[w] &= 2 * w + 1 < valid ? 0xffffffffu : 2 * w < valid ? 0x0000ffffu : 0u;
+  return v;
 }
 
 /* B operand for k rows kbase + 8g .. +7 of column n0 + c. */
@@ -103,7 +169,7 @@ TM_DEV uint32_t g_pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, t2));
 }
 
-template <typename T, int EPI>
+template <typename T, int EPI, bool RAGGED>
 TM_DEV void gemm_fast(const TmGemmArgs &p) {
   typedef typename GVec8<T>::type v8;
   __shared__ __align__(1024) char lds_a0[A_TILE];
@@ -111,11 +177,13 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   __shared__ __align__(1024) char lds_a1[A_TILE];
   __shared__ __align__(1024) char lds_b1[B_TILE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  /* uniform in the ragged kernel, whose copy ranges are scalar arithmetic */
+  const int wave = RAGGED ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
   const int g = lane >> 4, c = lane & 15;
   const int wm = wave >> 2, wn = wave & 3; /* 2 x 4 waves */
 
-  const int mt = p.m / GBM, nt = p.n / GBN;
+  const int mt = (p.m + GBM - 1) / GBM, nt = (p.n + GBN - 1) / GBN;
   const int logical = g_xcd_remap(blockIdx.x, gridDim.x);
   constexpr int GROUP = 8;
   const int per_group = GROUP * nt;
@@ -127,10 +195,26 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   const int tile_n = in_group / gm;
   const int m0 = tile_m * GBM, n0 = tile_n * GBN;
 
-  const T *A = (const T *)p.a;
-  const T *B = (const T *)p.b;
-  T *C = (T *)p.c;
   const int64_t lda = p.sam, ldb = p.sbk, ldc = p.scm;
+  const T *A = (const T *)p.a + (int64_t)m0 * lda;
+  const T *B = (const T *)p.b + n0;
+  T *C = (T *)p.c;
+  const int a_rows = RAGGED ? min(p.m - m0, GBM) : GBM;
+  const int b_cols = RAGGED ? min(p.n - n0, GBN) : GBN;
+
+  const int va = a_lane_offset(lda, lane);
+  int vb[2];
+  b_lane_offsets(ldb, wave, lane, vb);
+  auto stage = [&](char *ta, char *tb, int kb) {
+    const int k0 = kb * GBK;
+    if (RAGGED) {
+      stage_a(A + k0, lda, a_rows, p.k - k0, va, ta, wave);
+      stage_b(B + (int64_t)k0 * ldb, ldb, p.k - k0, b_cols, vb, tb, wave);
+    } else {
+      stage_a_global(A, lda, k0, ta, wave, lane);
+      stage_b_global(B, ldb, k0, tb, wave, lane);
+    }
+  };
 
   f32x4 acc[8][4];
 #pragma unroll
@@ -138,17 +222,16 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  const int ksteps = p.k / GBK;
-  stage_a<T>(A, lda, m0, 0, lds_a0, wave, lane);
-  stage_b<T>(B, ldb, 0, n0, lds_b0, wave, lane);
+  const int ksteps = (p.k + GBK - 1) / GBK;
+  stage(lds_a0, lds_b0, 0);
   g_wait_vmem();
   __syncthreads();
 
-  auto step = [&](const char *ca, const char *cb, char *na, char *nb, int kb) {
-    if (kb + 1 < ksteps) {
-      stage_a<T>(A, lda, m0, (kb + 1) * GBK, na, wave, lane);
-      stage_b<T>(B, ldb, (kb + 1) * GBK, n0, nb, wave, lane);
-    }
+  /* LAST (ragged K only): A's k columns at or past K are zeroed in registers;
+   * B's rows past K were copied as zeros by the range check. */
+  auto step = [&](auto last_tag, const char *ca, const char *cb, char *na, char *nb, int kb) {
+    constexpr bool LAST = decltype(last_tag)::value;
+    if (!LAST && kb + 1 < ksteps) stage(na, nb, kb + 1);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       v8 bf[4];
@@ -157,19 +240,33 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
         bf[j] = __builtin_bit_cast(v8, read_b_operand(cb, ks * 32, wn * 64 + j * 16, g, c));
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const v8 af = __builtin_bit_cast(
-            v8, *(const u32x4 *)(ca + a_off(wm * 128 + i * 16 + c, ks * 4 + g)));
+        u32x4 a = *(const u32x4 *)(ca + a_off(wm * 128 + i * 16 + c, ks * 4 + g));
+        if (LAST) a = keep_first(a, p.k - kb * GBK - ks * 32 - 8 * g);
+        const v8 af = __builtin_bit_cast(v8, a);
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma_16x16x32(bf[j], af, acc[i][j]);
       }
+      /* the last step has no copy in flight to pace it: keep its operand
+       * reads from all being hoisted ahead of the MFMAs (registers) */
+      if (LAST) __builtin_amdgcn_sched_barrier(0);
     }
-    g_wait_vmem();
-    __syncthreads();
+    if (!LAST) {
+      g_wait_vmem();
+      __syncthreads();
+    }
   };
+  using Full = std::integral_constant<bool, false>;
+  using Last = std::integral_constant<bool, true>;
 
-  for (int kb = 0; kb < ksteps; kb += 2) {
-    step(lds_a0, lds_b0, lds_a1, lds_b1, kb);
-    if (kb + 1 < ksteps) step(lds_a1, lds_b1, lds_a0, lds_b0, kb + 1);
+  /* with a ragged K the last step runs masked */
+  const int kfull = RAGGED && p.k % GBK ? ksteps - 1 : ksteps;
+  for (int kb = 0; kb < kfull; kb += 2) {
+    step(Full{}, lds_a0, lds_b0, lds_a1, lds_b1, kb);
+    if (kb + 1 < kfull) step(Full{}, lds_a1, lds_b1, lds_a0, lds_b0, kb + 1);
+  }
+  if (RAGGED && kfull < ksteps) {
+    const bool odd = kfull & 1;
+    step(Last{}, odd ? lds_a1 : lds_a0, odd ? lds_b1 : lds_b0, nullptr, nullptr, kfull);
   }
 
   /* acc[i][j] is the C^T tile: lane holds row m0 + wm*128 + i*16 + c,
@@ -180,13 +277,14 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      bias[j][r] = EPI == EPI_BIAS_RELU
-                       ? to_f32(((const T *)p.bias)[n0 + wn * 64 + j * 16 + 4 * g + r])
-                       : 0.f;
+    for (int r = 0; r < 4; ++r) {
+      const int n = n0 + wn * 64 + j * 16 + 4 * g + r;
+      bias[j][r] = EPI == EPI_BIAS_RELU && (!RAGGED || n < p.n) ? to_f32(((const T *)p.bias)[n]) : 0.f;
+    }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int m = m0 + wm * 128 + i * 16 + c;
+    if (RAGGED && m >= p.m) continue;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int n = n0 + wn * 64 + j * 16 + 4 * g;
@@ -194,20 +292,33 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         v[r] = EPI == EPI_BIAS_RELU ? fmaxf(acc[i][j][r] + bias[j][r], 0.f) : acc[i][j][r];
-      u32x2 w;
-      w[0] = g_pack2<T>(v[0], v[1]);
-      w[1] = g_pack2<T>(v[2], v[3]);
-      *(u32x2 *)(C + (int64_t)m * ldc + n) = w;
+      T *dst = C + (int64_t)m * ldc + n;
+      if (!RAGGED || n + 4 <= p.n) {
+        u32x2 w;
+        w[0] = g_pack2<T>(v[0], v[1]);
+        w[1] = g_pack2<T>(v[2], v[3]);
+        *(u32x2 *)dst = w;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < p.n) dst[r] = (T)v[r];
+      }
     }
   }
 }
 
-#define TM_GEMM_FAST(T, TN)                                                                \
-  extern "C" __global__ __launch_bounds__(512) void tm_gemm_fast_##TN(TmGemmArgs p) {        \
-    gemm_fast<T, EPI_NONE>(p);                                                               \
-  }                                                                                          \
-  extern "C" __global__ __launch_bounds__(512) void tm_sae_fast_##TN(TmGemmArgs p) {         \
-    gemm_fast<T, EPI_BIAS_RELU>(p);                                                          \
+#define TM_GEMM_FAST(T, TN)                                                                 \
+  extern "C" __global__ __launch_bounds__(512) void tm_gemm_fast_##TN(TmGemmArgs p) {         \
+    gemm_fast<T, EPI_NONE, false>(p);                                                         \
+  }                                                                                           \
+  extern "C" __global__ __launch_bounds__(512) void tm_gemm_ragged_##TN(TmGemmArgs p) {       \
+    gemm_fast<T, EPI_NONE, true>(p);                                                          \
+  }                                                                                           \
+  extern "C" __global__ __launch_bounds__(512) void tm_sae_fast_##TN(TmGemmArgs p) {          \
+    gemm_fast<T, EPI_BIAS_RELU, false>(p);                                                    \
+  }                                                                                           \
+  extern "C" __global__ __launch_bounds__(512) void tm_sae_ragged_##TN(TmGemmArgs p) {        \
+    gemm_fast<T, EPI_BIAS_RELU, true>(p);                                                     \
   }
 TM_GEMM_FAST(bf16_t, bf16)
 TM_GEMM_FAST(f16_t, f16)

@@ -533,19 +533,23 @@ void validate_attn_common(const char *name, int64_t heads, int32_t stride_head,
   if (heads > 65535) throw TmError(format("%s: %lld heads exceeds 65535", name, (long long)heads));
 }
 
-/* Kernel choice shared by matmul_kernel and sae_encode_kernel: the specialised
- * kernel takes 16-bit elements, row-major operands with unit inner stride and
- * 16-byte aligned rows, in whole 256 x 256 x 64 tiles; anything else runs the
- * generic 64 x 64 kernel. */
+/* Kernel choice shared by matmul_kernel and sae_encode_kernel.  The
+ * specialised kernels take 16-bit elements and row-major operands with unit
+ * inner stride, 16-byte aligned rows of A and B, 8-byte aligned rows of C,
+ * and rows no shorter than the matrix (lda >= K, ldb >= N): whole 256 x 256 x
+ * 64 tiles run the aligned kernel, any other M, N, K the ragged one, whose
+ * copies clip at the matrix's last row and whose last k-step and stores are
+ * masked.  Anything else runs the generic 64 x 64 kernel. */
 void choose_gemm(Plan &plan, const TmGemmArgs &p, const BuiltinSpec &spec, const char *family) {
   const char *el = element_name(spec.element);
   const bool fast = fast_paths_enabled() && spec.element != Element::F32 && p.sak == 1 &&
-                    p.sbn == 1 && p.scn == 1 && p.m % 256 == 0 && p.n % 256 == 0 &&
-                    p.k % 64 == 0 && p.k > 0 && p.sam % 8 == 0 && p.sbk % 8 == 0 &&
-                    p.scm % 8 == 0;
+                    p.sbn == 1 && p.scn == 1 && p.k > 0 && p.sam % 8 == 0 && p.sbk % 8 == 0 &&
+                    p.scm % 4 == 0 && p.sam >= p.k && p.sbk >= p.n &&
+                    p.sam <= (1 << 26) && p.sbk <= (1 << 26);
   if (fast) {
-    plan.variant = format("tm_%s_fast_%s", family, el);
-    plan.grid[0] = (unsigned)((p.m / 256) * (p.n / 256));
+    const bool whole = p.m % 256 == 0 && p.n % 256 == 0 && p.k % 64 == 0;
+    plan.variant = format("tm_%s_%s_%s", family, whole ? "fast" : "ragged", el);
+    plan.grid[0] = (unsigned)(cdiv(p.m, 256) * cdiv(p.n, 256));
     plan.block = 512;
   } else {
     plan.variant = format("tm_%s_generic_%s", family, el);
@@ -1269,7 +1273,12 @@ int64_t tm_alloc_buffer(int64_t length) {
     throw TmError(format("buffer length must be positive, got %lld", (long long)length));
   require_device();
   auto buf = std::make_shared<Buffer>();
-  hipError_t status = hipMalloc(&buf->ptr, (size_t)length);
+  /* Padded to 256 bytes: the GEMM's 16-byte tile copies may read up to 14
+   * bytes past the end of a matrix whose rows are not a multiple of 8
+   * elements (those bytes feed only outputs that are not stored). */
+  if (length > INT64_MAX - 255)
+    throw TmError(format("could not allocate a %lld-byte device buffer (too large)", (long long)length));
+  hipError_t status = hipMalloc(&buf->ptr, (size_t)((length + 255) & ~(int64_t)255));
   if (status != hipSuccess) {
     buf->ptr = nullptr;
     (void)hipGetLastError();
