@@ -233,6 +233,61 @@ def bench_sae(core, ops, rows, model, features, warmup, sample_ms):
     return ms, variant
 
 
+def bench_latency_configs(core, ops, sample_ms):
+    """Configs 1 and 2, the reference's latency-bound cases, timed as a caller
+    sees them.  Config 1: fp32 GEMM 256^3 on U[-1, 1] inputs, one dispatch
+    (device time from HIP events, and the wall time of one synchronous
+    tm_launch).  Config 2: the training loop of attention_training.py:312-329
+    at B1 H2 S96 D64 fp32, scale 1/8, lr 1e-3 on 0.5*||O - W||^2: per step,
+    upload Q/K/V, forward, read O, upload dO = O - W, backward, read the
+    gradients, SGD on the host -- wall time per step, and the device time of
+    its four dispatches."""
+    from triton_metal.buffer import DeviceBuffer
+    rng = np.random.default_rng(0)
+    a = DeviceBuffer.from_numpy(rng.uniform(-1, 1, (256, 256)).astype(np.float32), "float32")
+    b = DeviceBuffer.from_numpy(rng.uniform(-1, 1, (256, 256)).astype(np.float32), "float32")
+    c = DeviceBuffer((256, 256), "float32")
+    try:
+        kernel = ops.library("f32").kernels["matmul_kernel"]
+        grid, kinds, values = ops.matmul_args(a, b, c, 256, 256, 256)
+        device_ms = kernel_ms(core, kernel, grid, kinds, values, sample_ms)
+        for _ in range(20):
+            core.launch(kernel, grid, 128, kinds, values)
+        t0 = time.perf_counter()
+        for _ in range(200):
+            core.launch(kernel, grid, 128, kinds, values)
+        launch_us = (time.perf_counter() - t0) / 200 * 1e6
+    finally:
+        for x in (a, b, c):
+            x.free()
+    config1 = {"device_us": round(device_ms * 1e3, 2), "launch_us": round(launch_us, 2),
+               "tflops": round(gemm_flops(256, 256, 256) / (device_ms * 1e-3) / 1e12, 3),
+               "variant": core.kernel_variant(kernel)}
+
+    q, k, v, w = (rng.standard_normal((2, 96, 64), dtype=np.float32) * np.float32(0.1)
+                  for _ in range(4))
+    layer = ops.AttentionLayer(2, 96, 64, "f32", scale=1 / 8)
+    try:
+        def train_step(q, k, v):
+            o, _ = layer.forward(q, k, v)
+            d_out = o - w
+            dq, dk, dv = layer.backward(d_out)
+            return q - 1e-3 * dq, k - 1e-3 * dk, v - 1e-3 * dv
+        for _ in range(2):
+            q, k, v = train_step(q, k, v)
+        t0 = time.perf_counter()
+        for _ in range(8):
+            q, k, v = train_step(q, k, v)
+        step_ms = (time.perf_counter() - t0) / 8 * 1e3
+    finally:
+        layer.free()
+    _, kernels = bench_attention(core, ops, 1, 2, 96, 64, False, 0, 2, sample_ms, element="f32")
+    config2 = {"step_ms": round(step_ms, 4),
+               "device_us": round(sum(r["ms"] for r in kernels.values()) * 1e3, 2),
+               "dispatches_per_step": 4}
+    return config1, config2
+
+
 def cpu_baseline(target_seconds):
     """The oracle's float32 BLAS restatement of the reference's attention forward
     and backward (oracle.reference.attention_head_f32; attention_training.py:
@@ -388,6 +443,9 @@ def main():
                 "bwd_tflops": round(attention_flops(heads, seq, 64, False, backward=True)
                                     / (ms_b * 1e-3) / 1e12, 3),
                 "fwd_ms": round(ms_f, 4), "bwd_ms": round(ms_b, 4)}
+        config1, config2 = bench_latency_configs(core, ops, args.sample_ms)
+        ref["config1_gemm_f32_256"] = config1
+        ref["config2_training_step_f32"] = config2
         components["reference_shapes_f32"] = ref
     if args.only in ("all", "gemm"):
         n = 8192

@@ -20,10 +20,14 @@
  * matmul_kernel: C = A @ B, masked in M, N and K, f32 accumulation, output in
  * the element type (GEMMKernel.swift:28-174; matmul.py:20-44).
  * 64x64 output tile per 256-thread workgroup, 4 waves in 2x2, 32x32 per wave.
+ * K advances 32 at a time; the next k-slice's global loads are issued into
+ * registers before the current slice's MFMAs, so their latency overlaps the
+ * contraction (one barrier-separated LDS store per slice).
  * ------------------------------------------------------------------------- */
 template <typename T, int EPI>
 TM_DEV void gemm_generic(const TmGemmArgs &p) {
-  constexpr int BM = 64, BN = 64, BK = 16;
+  constexpr int BM = 64, BN = 64, BK = 32;
+  constexpr int PER = BM * BK / 256; /* elements of A (and of B) per thread per slice */
   __shared__ float As[BM][BK + 1];
   __shared__ float Bs[BK][BN + 4];
   const T *A = (const T *)p.a;
@@ -38,22 +42,33 @@ TM_DEV void gemm_generic(const TmGemmArgs &p) {
   for (int i = 0; i < 2; ++i)
     for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
+  /* element e = tid + 256 * i of a slice: A row e / BK, column e % BK (k
+   * fastest, so a wave reads runs along A's rows); B row e / BN, column e % BN */
+  float ra[PER], rb[PER];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + 256 * i;
+      const int gm = m0 + e / BK, gk = k0 + e % BK;
+      ra[i] = (gm < p.m && gk < p.k) ? to_f32(A[(int64_t)gm * p.sam + (int64_t)gk * p.sak]) : 0.f;
+      const int kk = k0 + e / BN, gn = n0 + e % BN;
+      rb[i] = (kk < p.k && gn < p.n) ? to_f32(B[(int64_t)kk * p.sbk + (int64_t)gn * p.sbn]) : 0.f;
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + 256 * i;
+      As[e / BK][e % BK] = ra[i];
+      Bs[e / BN][e % BN] = rb[i];
+    }
+  };
+
+  if (p.k > 0) load(0);
   for (int k0 = 0; k0 < p.k; k0 += BK) {
-    for (int e = tid; e < BM * BK; e += 256) {
-      const int r = e / BK, kk = e % BK;
-      const int gm = m0 + r, gk = k0 + kk;
-      As[r][kk] = (gm < p.m && gk < p.k)
-                      ? to_f32(A[(int64_t)gm * p.sam + (int64_t)gk * p.sak])
-                      : 0.f;
-    }
-    for (int e = tid; e < BK * BN; e += 256) {
-      const int kk = e / BN, cc = e % BN;
-      const int gk = k0 + kk, gn = n0 + cc;
-      Bs[kk][cc] = (gk < p.k && gn < p.n)
-                       ? to_f32(B[(int64_t)gk * p.sbk + (int64_t)gn * p.sbn])
-                       : 0.f;
-    }
+    store();
     __syncthreads();
+    if (k0 + BK < p.k) load(k0 + BK);
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 4) {
       float a[2], b[2];
