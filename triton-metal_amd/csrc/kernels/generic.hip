@@ -104,6 +104,38 @@ TM_DEV void gemm_generic(const TmGemmArgs &p) {
       }
 }
 
+/* Two [ROWS x DP] row tiles of one head (rows r0 .., columns < D, zeros
+ * outside the sequence and the head dimension) staged HBM -> registers -> LDS
+ * as f32 with row stride DP + 1.  The attention loops call load() for the
+ * next block right after the current block is in LDS, so the global reads'
+ * latency overlaps the current block's MFMAs; store() writes them out after
+ * the barrier that ends the current block. */
+template <typename T, int ROWS, int DP>
+struct TileStager {
+  static constexpr int PER = ROWS * DP / 256;
+  static_assert(ROWS * DP % 256 == 0, "whole elements per thread");
+  float ra[PER], rb[PER];
+  TM_DEV void load(const T *a, const T *b, int r0, int n, int D, int64_t ss, int tid) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + 256 * i;
+      const int r = r0 + e / DP, cc = e % DP;
+      const bool ok = r < n && cc < D;
+      const int64_t off = (int64_t)r * ss + cc;
+      ra[i] = ok ? to_f32(a[off]) : 0.f;
+      rb[i] = ok ? to_f32(b[off]) : 0.f;
+    }
+  }
+  TM_DEV void store(float *as, float *bs, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + 256 * i;
+      as[(e / DP) * (DP + 1) + e % DP] = ra[i];
+      bs[(e / DP) * (DP + 1) + e % DP] = rb[i];
+    }
+  }
+};
+
 /* ---------------------------------------------------------------------------
  * attn_fwd: FlashAttention-2 forward with the online softmax in the exp2
  * domain (AttentionKernel.swift:40-250; attention_training.py:37-71).
@@ -143,17 +175,13 @@ TM_DEV void attn_fwd_generic(const TmAttnFwdArgs &p) {
   for (int i = 0; i < DP / 16; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   const int kend = CAUSAL ? min(n, q0 + BM) : n;
+  TileStager<T, BN, DP> kv;
+  if (kend > 0) kv.load(K, V, 0, n, D, p.stride_seq, tid);
   for (int k0 = 0; k0 < kend; k0 += BN) {
     __syncthreads();
-    for (int e = tid; e < BN * DP; e += 256) {
-      const int r = e / DP, cc = e % DP;
-      const int kj = k0 + r;
-      const bool ok = kj < n && cc < D;
-      const int64_t off = (int64_t)kj * p.stride_seq + cc;
-      Ks[r * LD + cc] = ok ? to_f32(K[off]) : 0.f;
-      Vs[r * LD + cc] = ok ? to_f32(V[off]) : 0.f;
-    }
+    kv.store(Ks, Vs, tid);
     __syncthreads();
+    if (k0 + BN < kend) kv.load(K, V, k0 + BN, n, D, p.stride_seq, tid);
 
     float sc[2][4];
     float mx = TM_NEG_INF;
@@ -278,17 +306,13 @@ TM_DEV void attn_dq_generic(const TmAttnDqArgs &p) {
   for (int i = 0; i < DP / 16; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   const int kend = CAUSAL ? min(n, q0 + BM) : n;
+  TileStager<T, BN, DP> kv;
+  if (kend > 0) kv.load(K, V, 0, n, D, p.stride_seq, tid);
   for (int k0 = 0; k0 < kend; k0 += BN) {
     __syncthreads();
-    for (int e = tid; e < BN * DP; e += 256) {
-      const int r = e / DP, cc = e % DP;
-      const int kj = k0 + r;
-      const bool ok = kj < n && cc < D;
-      const int64_t off = (int64_t)kj * p.stride_seq + cc;
-      Ks[r * LD + cc] = ok ? to_f32(K[off]) : 0.f;
-      Vs[r * LD + cc] = ok ? to_f32(V[off]) : 0.f;
-    }
+    kv.store(Ks, Vs, tid);
     __syncthreads();
+    if (k0 + BN < kend) kv.load(K, V, k0 + BN, n, D, p.stride_seq, tid);
 
     float ds[2][4];
 #pragma unroll
@@ -376,22 +400,29 @@ TM_DEV void attn_dkdv_generic(const TmAttnDkdvArgs &p) {
   }
 
   const int qstart = CAUSAL ? (k0 / BM) * BM : 0;
+  TileStager<T, BM, DP> qdo;
+  float l_next = 0.f, d_next = 0.f; /* thread tid < BM: L and Delta of row tid */
+  auto load_stats = [&](int q0) {
+    const int qi = q0 + tid;
+    l_next = tid < BM && qi < n ? Lrow[qi] : 0.f;
+    d_next = tid < BM && qi < n ? Drow[qi] : 0.f;
+  };
+  if (qstart < n) {
+    qdo.load(Q, dO, qstart, n, D, p.stride_seq, tid);
+    load_stats(qstart);
+  }
   for (int q0 = qstart; q0 < n; q0 += BM) {
     __syncthreads();
-    for (int e = tid; e < BM * DP; e += 256) {
-      const int r = e / DP, cc = e % DP;
-      const int qi = q0 + r;
-      const bool ok = qi < n && cc < D;
-      const int64_t off = (int64_t)qi * p.stride_seq + cc;
-      Qs[r * LD + cc] = ok ? to_f32(Q[off]) : 0.f;
-      dOs[r * LD + cc] = ok ? to_f32(dO[off]) : 0.f;
-    }
+    qdo.store(Qs, dOs, tid);
     if (tid < BM) {
-      const int qi = q0 + tid;
-      Ls[tid] = qi < n ? Lrow[qi] : 0.f;
-      Ds[tid] = qi < n ? Drow[qi] : 0.f;
+      Ls[tid] = l_next;
+      Ds[tid] = d_next;
     }
     __syncthreads();
+    if (q0 + BM < n) {
+      qdo.load(Q, dO, q0 + BM, n, D, p.stride_seq, tid);
+      load_stats(q0 + BM);
+    }
 
     float pt[2][4], dst[2][4];
 #pragma unroll
