@@ -196,6 +196,29 @@ def test_builtin_launch_checks_buffer_extents(core, device):
         core.release_library(lib)
 
 
+@pytest.mark.parametrize("builtin,args", [
+    # M = 2^31 - 1 rows at a stride of 2^31 - 1: the extent in bytes exceeds 2^63
+    ("matmul_kernel", [2**31 - 1, 1, 1, 2**31 - 1, 1, 1, 1, 1, 1]),
+    # 65535 heads of 2^31 - 1 rows at stride 2^31 - 1
+    ("attn_bwd_preprocess", [2**31 - 1, 2**31 - 1, 2**31 - 1, 2**31 - 1]),
+])
+def test_extent_checks_do_not_wrap(core, device, builtin, args):
+    """Sizes whose byte extent overflows 64 bits are refused on the host, not
+    wrapped into a small number that passes the check."""
+    lib = core.compile_msl("builtin element=f32")
+    kernel = core.load_kernel(lib, builtin)
+    small = core.alloc_buffer(64)
+    try:
+        nbuf = 3
+        grid = (1, 1, 1) if builtin == "matmul_kernel" else (1, 65535, 1)
+        with pytest.raises(RuntimeError, match="needs 9223372036854775807 bytes but its buffer holds 64"):
+            core.launch(kernel, grid, 128, [0] * nbuf + [1] * len(args), [small] * nbuf + args)
+    finally:
+        core.free_buffer(small)
+        core.release_kernel(kernel)
+        core.release_library(lib)
+
+
 BLOCK_KERNEL = r"""
 #include <hip/hip_runtime.h>
 struct Block { const void *a, *b; void *c; int m, n, k, s0, s1, s2, s3, s4, s5; const void *bias; };

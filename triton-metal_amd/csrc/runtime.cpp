@@ -458,17 +458,25 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 /* Elements a strided 2-D access touches, from element 0: the host-side proof
  * that a kernel stays inside its buffer. */
+/* Saturates at INT64_MAX (int32 sizes and strides cannot reach it in a
+ * buffer that exists, but a caller's arithmetic must not wrap a check). */
 int64_t extent(int64_t rows, int64_t row_stride, int64_t cols, int64_t col_stride) {
   if (rows <= 0 || cols <= 0) return 0;
-  return (rows - 1) * row_stride + (cols - 1) * col_stride + 1;
+  const __int128 e = (__int128)(rows - 1) * row_stride + (__int128)(cols - 1) * col_stride + 1;
+  return e > (__int128)INT64_MAX ? INT64_MAX : (int64_t)e;
 }
+
+/* a + b for non-negative sizes, saturating like extent() */
+int64_t sat_add(int64_t a, int64_t b) { return a > INT64_MAX - b ? INT64_MAX : a + b; }
 
 void require_extent(const Arg &a, int64_t elements, int esize, const char *kernel, int index,
                     const char *what) {
-  const int64_t need = elements * esize;
-  if (need > a.buffer->length)
+  if (elements > a.buffer->length / esize) {
+    const __int128 need = (__int128)elements * esize;
     throw TmError(format("%s argument %d (%s) needs %lld bytes but its buffer holds %lld", kernel,
-                         index, what, (long long)need, (long long)a.buffer->length));
+                         index, what, need > (__int128)INT64_MAX ? (long long)INT64_MAX : (long long)need,
+                         (long long)a.buffer->length));
+  }
 }
 
 void require_nonneg(int64_t v, const char *kernel, const char *what) {
@@ -654,8 +662,8 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
       const char *nm = info.name;
       validate_attn_common(nm, heads, p.stride_head, p.stride_seq, p.n_ctx, spec.head_dim);
       const int64_t ext = heads > 0 && p.n_ctx > 0
-                              ? (heads - 1) * (int64_t)p.stride_head +
-                                    extent(p.n_ctx, p.stride_seq, spec.head_dim, 1)
+                              ? sat_add((heads - 1) * (int64_t)p.stride_head,
+                                    extent(p.n_ctx, p.stride_seq, spec.head_dim, 1))
                               : 0;
       for (int i = 0; i < 4; ++i) require_extent(args[i], ext, es, nm, i, "Q/K/V/O");
       if (args.size() == 10) {
@@ -700,8 +708,8 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
       validate_attn_common(nm, heads, p.stride_head, p.stride_seq, p.n_ctx, spec.head_dim);
       require_nonneg(p.stride_lse, nm, "stride_lse");
       const int64_t ext = heads > 0 && p.n_ctx > 0
-                              ? (heads - 1) * (int64_t)p.stride_head +
-                                    extent(p.n_ctx, p.stride_seq, spec.head_dim, 1)
+                              ? sat_add((heads - 1) * (int64_t)p.stride_head,
+                                    extent(p.n_ctx, p.stride_seq, spec.head_dim, 1))
                               : 0;
       require_extent(args[0], ext, es, nm, 0, "O");
       require_extent(args[1], ext, es, nm, 1, "dO");
@@ -737,8 +745,8 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
       validate_attn_common(nm, heads, stride_head, stride_seq, n_ctx, spec.head_dim);
       require_nonneg(stride_lse, nm, "stride_lse");
       const int64_t ext = heads > 0 && n_ctx > 0
-                              ? (heads - 1) * (int64_t)stride_head +
-                                    extent(n_ctx, stride_seq, spec.head_dim, 1)
+                              ? sat_add((heads - 1) * (int64_t)stride_head,
+                                    extent(n_ctx, stride_seq, spec.head_dim, 1))
                               : 0;
       for (int i = 0; i < first_stat; ++i) require_extent(args[i], ext, es, nm, i, "tensor");
       const int64_t sext =
