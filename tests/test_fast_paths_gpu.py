@@ -163,15 +163,25 @@ def _gemm(m, n, k, element, lda=None, ldb=None, ldc=None, seed=0, poison=False, 
     return c, want, variant
 
 
+def _tile_suffix(m, n, cus=256):
+    """The planner's tile choice on an MI355X (256 compute units): rounds of
+    resident 256 x 256 tiles (one per CU) at 31 against rounds of 128 x 128
+    pairs (two per CU) at 21; "_t128" names the smaller tile."""
+    cd = lambda a, b: -(-a // b)
+    big = cd(cd(m, 256) * cd(n, 256), cus) * 31 <= cd(cd(m, 128) * cd(n, 128), 2 * cus) * 21
+    return "" if big else "_t128"
 @pytest.mark.parametrize("element", ["bf16", "f16"])
-@pytest.mark.parametrize("m,n,k,lda,ldb,ldc", [
-    (256, 512, 64, None, None, None),
-    (512, 256, 192, None, None, None),
-    (768, 1024, 320, 328, 1032, 1040),   # padded leading dimensions, 16-byte aligned
+@pytest.mark.parametrize("m,n,k,lda,ldb,ldc,tile", [
+    (256, 512, 64, None, None, None, "_t128"),
+    (512, 256, 192, None, None, None, "_t128"),
+    (768, 1024, 320, 328, 1032, 1040, "_t128"),   # padded leading dimensions, 16-byte aligned
+    (4096, 4096, 128, None, None, None, ""),
+    (4096, 4096, 64, 72, 4104, 4100, ""),
 ])
-def test_fast_gemm_shapes_and_strides(element, m, n, k, lda, ldb, ldc, device):
+def test_fast_gemm_shapes_and_strides(element, m, n, k, lda, ldb, ldc, tile, device):
     c, want, variant = _gemm(m, n, k, element, lda, ldb, ldc)
-    assert variant == f"tm_gemm_fast_{element}"
+    assert tile == _tile_suffix(m, n)
+    assert variant == f"tm_gemm_fast{tile}_{element}"
     assert T.hybrid_error(c[:, :n], want) <= 2e-2
     if ldc:
         assert np.all(c[:, n:] == -7.0)
@@ -186,13 +196,16 @@ def test_fast_gemm_shapes_and_strides(element, m, n, k, lda, ldb, ldc, device):
     (1, 1, 1, 8, 8, 4),                  # one element
     (300, 1000, 136, None, None, None),
     (513, 777, 1000, 1000, 784, 780),
+    (4000, 4100, 200, 200, 4104, 4100),  # 272 tiles of 256 x 256
+    (4096, 4096, 72, None, None, None),  # whole 256 x 256 tiles, ragged K
 ])
 def test_ragged_gemm(element, m, n, k, lda, ldb, ldc, device):
     """Any M, N, K with 16-byte aligned rows of A and B run the ragged
     specialised kernel: masked to the matrix, with inf/NaN in the operands'
     padding and sentinel rows and columns around C."""
     c, want, variant = _gemm(m, n, k, element, lda, ldb, ldc, poison=True, extra_rows=3)
-    assert variant == f"tm_gemm_ragged_{element}"
+    tile = _tile_suffix(m, n)
+    assert variant == f"tm_gemm_ragged{tile}_{element}"
     assert np.all(np.isfinite(c[:m, :n]))
     assert T.hybrid_error(c[:m, :n], want) <= 2e-2
     assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)
@@ -201,8 +214,9 @@ def test_ragged_gemm(element, m, n, k, lda, ldb, ldc, device):
 @pytest.mark.parametrize("m,n,k,lda,ldb,variant", [
     (256, 256, 60, None, None, "generic"),    # rows of A not 16-byte aligned
     (300, 200, 100, None, None, "generic"),
-    (255, 256, 64, None, None, "ragged"),
-    (512, 256, 128, None, None, "fast"),
+    (255, 256, 64, None, None, "ragged_t128"),
+    (512, 256, 128, None, None, "fast_t128"),
+    (4096, 4096, 64, None, None, "fast"),
 ])
 def test_gemm_kernel_choice(m, n, k, lda, ldb, variant, device):
     c, want, got = _gemm(m, n, k, "bf16", lda, ldb)

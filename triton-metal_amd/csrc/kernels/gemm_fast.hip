@@ -48,9 +48,7 @@ TM_DEV int g_xcd_remap(int wg, int nwg) {
   return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
 }
 
-constexpr int GBM = 256, GBN = 256, GBK = 64;
-constexpr int A_TILE = GBM * GBK * 2; /* 32 KB: 256 rows of 128 bytes */
-constexpr int B_TILE = GBK * GBN * 2; /* 32 KB: 64 rows of 512 bytes */
+constexpr int GBK = 64;
 
 /* A tile: 128-byte rows (8 chunks), read only by ds_read_b128 of 16
  * consecutive rows at one chunk: the key row & 7 gives those reads no bank
@@ -59,11 +57,13 @@ constexpr int B_TILE = GBK * GBN * 2; /* 32 KB: 64 rows of 512 bytes */
 TM_DEV int a_swz(int row) { return row & 7; }
 TM_DEV int a_off(int row, int chunk) { return row * 128 + ((chunk ^ a_swz(row)) << 4); }
 
-/* B tile: 512-byte rows (32 chunks).  A transpose read touches rows
+/* B tile: BN-element rows (2 BN bytes: 32 or 16 chunks, a multiple of the
+ * 256-byte bank width either way).  A transpose read touches rows
  * k0 + 8g + {0..3} (and +4) at one chunk pair; the even key separates the
  * pairs of the 8 rows served together. */
 TM_DEV int b_swz(int row) { return ((row & 3) | ((row >> 1) & 4)) << 1; }
-TM_DEV int b_off(int row, int chunk) { return row * 512 + ((chunk ^ b_swz(row)) << 4); }
+template <int BN>
+TM_DEV int b_off(int row, int chunk) { return row * (2 * BN) + ((chunk ^ b_swz(row)) << 4); }
 
 /* Each copy instruction moves a few whole rows of a tile through a buffer
  * resource based at its first row, whose range ends at the matrix's last
@@ -79,8 +79,8 @@ TM_DEV void copy_rows(const void *base, int rows_left, int64_t ld, int width, in
   lds_copy16_buffer(raw_buffer_rsrc(base, bytes), voff, lds_addr(slot));
 }
 
-/* A [256 x 64] tile, k0 = 0 at `a`: 32 instructions of 8 rows (4 per wave);
- * lane l copies row 8t + (l >> 3), source chunk (l & 7) ^ a_swz(row). */
+/* A [BM x 64] tile, k0 = 0 at `a`: BM / 8 instructions of 8 rows (4 per
+ * wave); lane l copies row 8t + (l >> 3), source chunk (l & 7) ^ a_swz(row). */
 template <typename T>
 TM_DEV void stage_a(const T *a, int64_t lda, int rows_left, int width, int voff, char *tile, int wave) {
 #pragma unroll
@@ -94,23 +94,28 @@ TM_DEV int a_lane_offset(int64_t lda, int lane) {
   return r * (int)lda * 2 + (((lane & 7) ^ a_swz(r)) << 4);
 }
 
-/* B [64 x 256] tile: 32 instructions of 2 rows (4 per wave); lane l copies
- * row 2t + (l >> 5), source chunk (l & 31) ^ b_swz(row).  For t = 4w + i,
- * b_swz(row) depends on the lane, w and i & 1 only. */
-template <typename T>
-TM_DEV void stage_b(const T *b, int64_t ldb, int rows_left, int width, const int (&voff)[2], char *tile,
+/* B [64 x BN] tile: BN / 8 instructions of RPI = 512 / BN rows (4 per
+ * wave); lane l copies row RPI t + l / CPR, source chunk (l % CPR) ^
+ * b_swz(row), CPR = BN / 8 chunks per row.  For t = 4w + i the key depends on
+ * the lane, w and i only, so each of the 4 offsets is fixed per lane. */
+template <typename T, int BN>
+TM_DEV void stage_b(const T *b, int64_t ldb, int rows_left, int width, const int (&voff)[4], char *tile,
                     int wave) {
+  constexpr int RPI = 512 / BN;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = wave * 4 + i;
-    copy_rows<2>(b + (int64_t)(t * 2) * ldb, rows_left - t * 2, ldb, width, voff[i & 1], tile + t * 1024);
+    copy_rows<RPI>(b + (int64_t)(t * RPI) * ldb, rows_left - t * RPI, ldb, width, voff[i],
+                   tile + t * 1024);
   }
 }
-TM_DEV void b_lane_offsets(int64_t ldb, int wave, int lane, int (&voff)[2]) {
-  const int h = lane >> 5;
+template <int BN>
+TM_DEV void b_lane_offsets(int64_t ldb, int wave, int lane, int (&voff)[4]) {
+  constexpr int RPI = 512 / BN, CPR = BN / 8;
+  const int h = lane / CPR;
 #pragma unroll
-  for (int e = 0; e < 2; ++e)
-    voff[e] = h * (int)ldb * 2 + (((lane & 31) ^ b_swz(wave * 8 + 2 * e + h)) << 4);
+  for (int i = 0; i < 4; ++i)
+    voff[i] = h * (int)ldb * 2 + (((lane % CPR) ^ b_swz((wave * 4 + i) * RPI + h)) << 4);
 }
 
 /* The aligned kernel's copies: every row and column of a tile is inside the
@@ -129,13 +134,14 @@ TM_DEV void stage_a_global(const T *a, int64_t lda, int k0, char *tile, int wave
   }
 }
 
-template <typename T>
+template <typename T, int BN>
 TM_DEV void stage_b_global(const T *b, int64_t ldb, int k0, char *tile, int wave, int lane) {
+  constexpr int RPI = 512 / BN, CPR = BN / 8;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = wave * 4 + i;
-    const int row = t * 2 + (lane >> 5);
-    const int chunk = (lane & 31) ^ b_swz(row);
+    const int row = t * RPI + lane / CPR;
+    const int chunk = (lane % CPR) ^ b_swz(row);
     global_rows_to_lds(b + (int64_t)(k0 + row) * ldb + chunk * 8, tile + t * 1024);
   }
 }
@@ -150,14 +156,15 @@ TM_DEV u32x4 keep_first(u32x4 v, int valid) {
 }
 
 /* B operand for k rows kbase + 8g .. +7 of column n0 + c. */
+template <int BN>
 TM_DEV u32x4 read_b_operand(const char *tile, int kbase, int n0, int g, int c) {
   const int n = n0 + 4 * (c & 3);
   const int chunk = n >> 3, half = (n >> 2) & 1;
   const int ra = kbase + 8 * g + (c >> 2), rb = ra + 4;
   const gs16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) gs16x4 *)(tile + b_off(ra, chunk) + (half << 3)));
+      (__attribute__((address_space(3))) gs16x4 *)(tile + b_off<BN>(ra, chunk) + (half << 3)));
   const gs16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) gs16x4 *)(tile + b_off(rb, chunk) + (half << 3)));
+      (__attribute__((address_space(3))) gs16x4 *)(tile + b_off<BN>(rb, chunk) + (half << 3)));
   const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
   return (u32x4){ua[0], ua[1], ub[0], ub[1]};
 }
@@ -169,9 +176,18 @@ TM_DEV uint32_t g_pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, t2));
 }
 
-template <typename T, int EPI, bool RAGGED>
+/* BM x BN tiles: 256 x 256 with 8 waves (2 x 4) of 128 x 64, or 128 x 128
+ * with 4 waves (2 x 2) of 64 x 64 for problems with fewer 256 x 256 tiles
+ * than compute units.  A wave's sub-tile is (BM / 2) x 64. */
+template <typename T, int EPI, bool RAGGED, int BM, int BN>
 TM_DEV void gemm_fast(const TmGemmArgs &p) {
   typedef typename GVec8<T>::type v8;
+  constexpr int GBM = BM, GBN = BN;
+  constexpr int A_TILE = BM * GBK * 2; /* BM rows of 128 bytes */
+  constexpr int B_TILE = GBK * BN * 2; /* 64 rows of 2 BN bytes */
+  constexpr int WN = BN / 64;          /* waves across N */
+  constexpr int MI = BM / 32;          /* 16-row tiles per wave */
+  static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 128), "tile shapes");
   __shared__ __align__(1024) char lds_a0[A_TILE];
   __shared__ __align__(1024) char lds_b0[B_TILE];
   __shared__ __align__(1024) char lds_a1[A_TILE];
@@ -181,7 +197,7 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   /* uniform in the ragged kernel, whose copy ranges are scalar arithmetic */
   const int wave = RAGGED ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
   const int g = lane >> 4, c = lane & 15;
-  const int wm = wave >> 2, wn = wave & 3; /* 2 x 4 waves */
+  const int wm = wave / WN, wn = wave % WN; /* 2 x WN waves */
 
   const int mt = (p.m + GBM - 1) / GBM, nt = (p.n + GBN - 1) / GBN;
   const int logical = g_xcd_remap(blockIdx.x, gridDim.x);
@@ -203,22 +219,22 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   const int b_cols = RAGGED ? min(p.n - n0, GBN) : GBN;
 
   const int va = a_lane_offset(lda, lane);
-  int vb[2];
-  b_lane_offsets(ldb, wave, lane, vb);
+  int vb[4];
+  b_lane_offsets<BN>(ldb, wave, lane, vb);
   auto stage = [&](char *ta, char *tb, int kb) {
     const int k0 = kb * GBK;
     if (RAGGED) {
       stage_a(A + k0, lda, a_rows, p.k - k0, va, ta, wave);
-      stage_b(B + (int64_t)k0 * ldb, ldb, p.k - k0, b_cols, vb, tb, wave);
+      stage_b<T, BN>(B + (int64_t)k0 * ldb, ldb, p.k - k0, b_cols, vb, tb, wave);
     } else {
       stage_a_global(A, lda, k0, ta, wave, lane);
-      stage_b_global(B, ldb, k0, tb, wave, lane);
+      stage_b_global<T, BN>(B, ldb, k0, tb, wave, lane);
     }
   };
 
-  f32x4 acc[8][4];
+  f32x4 acc[MI][4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
@@ -237,10 +253,10 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
       v8 bf[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        bf[j] = __builtin_bit_cast(v8, read_b_operand(cb, ks * 32, wn * 64 + j * 16, g, c));
+        bf[j] = __builtin_bit_cast(v8, read_b_operand<BN>(cb, ks * 32, wn * 64 + j * 16, g, c));
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        u32x4 a = *(const u32x4 *)(ca + a_off(wm * 128 + i * 16 + c, ks * 4 + g));
+      for (int i = 0; i < MI; ++i) {
+        u32x4 a = *(const u32x4 *)(ca + a_off(wm * (BM / 2) + i * 16 + c, ks * 4 + g));
         if (LAST) a = keep_first(a, p.k - kb * GBK - ks * 32 - 8 * g);
         const v8 af = __builtin_bit_cast(v8, a);
 #pragma unroll
@@ -269,7 +285,7 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
     step(Last{}, odd ? lds_a1 : lds_a0, odd ? lds_b1 : lds_b0, nullptr, nullptr, kfull);
   }
 
-  /* acc[i][j] is the C^T tile: lane holds row m0 + wm*128 + i*16 + c,
+  /* acc[i][j] is the C^T tile: lane holds row m0 + wm*BM/2 + i*16 + c,
    * columns n0 + wn*64 + j*16 + 4g .. +3 */
   /* The bias of the wave's 16 columns, loaded once before any store (the
    * compiler cannot move the loads across stores to C that might alias). */
@@ -282,8 +298,8 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
       bias[j][r] = EPI == EPI_BIAS_RELU && (!RAGGED || n < p.n) ? to_f32(((const T *)p.bias)[n]) : 0.f;
     }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int m = m0 + wm * 128 + i * 16 + c;
+  for (int i = 0; i < MI; ++i) {
+    const int m = m0 + wm * (BM / 2) + i * 16 + c;
     if (RAGGED && m >= p.m) continue;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -307,18 +323,18 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   }
 }
 
-#define TM_GEMM_FAST(T, TN)                                                                 \
-  extern "C" __global__ __launch_bounds__(512) void tm_gemm_fast_##TN(TmGemmArgs p) {         \
-    gemm_fast<T, EPI_NONE, false>(p);                                                         \
-  }                                                                                           \
-  extern "C" __global__ __launch_bounds__(512) void tm_gemm_ragged_##TN(TmGemmArgs p) {       \
-    gemm_fast<T, EPI_NONE, true>(p);                                                          \
-  }                                                                                           \
-  extern "C" __global__ __launch_bounds__(512) void tm_sae_fast_##TN(TmGemmArgs p) {          \
-    gemm_fast<T, EPI_BIAS_RELU, false>(p);                                                    \
-  }                                                                                           \
-  extern "C" __global__ __launch_bounds__(512) void tm_sae_ragged_##TN(TmGemmArgs p) {        \
-    gemm_fast<T, EPI_BIAS_RELU, true>(p);                                                     \
+#define TM_GEMM_ONE(NAME, T, EPI, RAGGED, TILE)                                             \
+  extern "C" __global__ __launch_bounds__(TILE * 2) void NAME(TmGemmArgs p) {                 \
+    gemm_fast<T, EPI, RAGGED, TILE, TILE>(p);                                                  \
   }
+#define TM_GEMM_FAST(T, TN)                                                 \
+  TM_GEMM_ONE(tm_gemm_fast_##TN, T, EPI_NONE, false, 256)                   \
+  TM_GEMM_ONE(tm_gemm_ragged_##TN, T, EPI_NONE, true, 256)                  \
+  TM_GEMM_ONE(tm_sae_fast_##TN, T, EPI_BIAS_RELU, false, 256)               \
+  TM_GEMM_ONE(tm_sae_ragged_##TN, T, EPI_BIAS_RELU, true, 256)              \
+  TM_GEMM_ONE(tm_gemm_fast_t128_##TN, T, EPI_NONE, false, 128)              \
+  TM_GEMM_ONE(tm_gemm_ragged_t128_##TN, T, EPI_NONE, true, 128)             \
+  TM_GEMM_ONE(tm_sae_fast_t128_##TN, T, EPI_BIAS_RELU, false, 128)          \
+  TM_GEMM_ONE(tm_sae_ragged_t128_##TN, T, EPI_BIAS_RELU, true, 128)
 TM_GEMM_FAST(bf16_t, bf16)
 TM_GEMM_FAST(f16_t, f16)
