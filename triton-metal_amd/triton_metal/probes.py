@@ -12,6 +12,8 @@ published peaks (256 CUs; dense bf16 MFMA 2.5 PFLOP/s = 4096 FLOP/clk/CU).
   atomic_add_f32 / rmw_f32        fp32 atomic adds vs plain read-add-write on
                                   coalesced [32 x 128] tiles (the dQ tile of a
                                   fused backward)
+  atomic_dq_config5               the dQ atomic adds alone of a fused backward
+                                  at config 5, in their real pattern
 
 Run: python bench.py --probes
 """
@@ -125,6 +127,19 @@ extern "C" __global__ __launch_bounds__(256) void probe_atomic(float *acc, int i
     for (int e = threadIdx.x; e < 4096; e += 256)
       __hip_atomic_fetch_add(acc + tile + e, 1.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+/* The dQ traffic of a fused single-kernel backward at config 5 (B4 H32
+ * S4096 D128 causal, 128 keys per workgroup, 32-query steps): workgroup
+ * (bh, kb) adds one [32 x 128] fp32 tile into dQ for every query block from
+ * its first key to the end -- 1.107e9 atomic adds in all, nothing else. */
+extern "C" __global__ __launch_bounds__(256) void probe_dq_atomics(float *dq, int seq) {
+  const int nkb = seq / 128;
+  const int bh = blockIdx.x / nkb, kb = blockIdx.x % nkb;
+  float *head = dq + (long)bh * seq * 128;
+  for (int q0 = kb * 128; q0 < seq; q0 += 32)
+    for (int e = threadIdx.x; e < 32 * 128; e += 256)
+      __hip_atomic_fetch_add(head + (long)q0 * 128 + e, 1.0f, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
 extern "C" __global__ __launch_bounds__(256) void probe_rmw(float *acc, int iters) {
   const long tile = (long)(blockIdx.x % 4096) * 4096;
   for (int r = 0; r < iters; ++r)
@@ -162,10 +177,29 @@ def run(iters=4096, workgroups=CUS * 16):
                              "total_per_s": float(f"{total:.4g}"),
                              "per_cu_clk": round(total / CUS / CLOCK_HZ, 2)}
             _core.release_kernel(kernel)
+        results["atomic_dq_config5"] = _dq_atomics(lib)
     finally:
         _core.free_buffer(scratch)
         _core.release_library(lib)
     return results
+
+
+def _dq_atomics(lib, heads=128, seq=4096):
+    """Time the dQ atomics alone of a fused backward at config 5: the lower
+    bound such a kernel would pay on top of its dK/dV work."""
+    kernel = _core.load_kernel(lib, "probe_dq_atomics")
+    dq = _core.alloc_buffer(heads * seq * 128 * 4)
+    try:
+        grid = (heads * (seq // 128), 1, 1)
+        args = ([_core.ARG_BUFFER, _core.ARG_I32], [dq, seq])
+        _core.launch(kernel, grid, 256, *args)
+        ms = _core.launch_timed(kernel, grid, 256, args[0], args[1], 3) / 3
+        adds = heads * 128 * sum(seq - 128 * kb for kb in range(seq // 128))
+    finally:
+        _core.free_buffer(dq)
+        _core.release_kernel(kernel)
+    return {"ms": round(ms, 4), "unit": "add", "adds": adds,
+            "total_per_s": float(f"{adds / (ms * 1e-3):.4g}")}
 
 
 if __name__ == "__main__":
