@@ -140,9 +140,42 @@ def test_config1_fp32_256_uniform(device):
     """Config 1: fp32 256^3, U[-1,1] from seed 0, 1e-5 (hybrid) vs fp64."""
     a = G.uniform((256, 256), seed=0)
     b = G.uniform((256, 256), seed=1)
-    c, _ = run_matmul(a.reshape(-1), b.reshape(-1), 256, 256, 256, (256, 1, 256, 1, 256, 1))
+    c, variant = run_matmul(a.reshape(-1), b.reshape(-1), 256, 256, 256, (256, 1, 256, 1, 256, 1))
+    assert variant == "tm_gemm_generic_f32"  # 4 tiles of 128 x 128: too few for the fp32 MFMA kernel
     want = a.astype(np.float64) @ b.astype(np.float64)
     assert T.hybrid_error(c.reshape(256, 256), want) <= 1e-5
+
+
+@pytest.mark.parametrize("m,n,k,lda,ldb,ldc,variant", [
+    (2048, 1024, 32, None, None, None, "fast"),      # 128 tiles: half the compute units
+    (1536, 2048, 96, 100, 2052, 2056, "fast"),      # padded, 16-byte aligned rows
+    (2048, 2048, 1024, None, None, None, "fast"),
+    (1024, 1024, 1024, None, None, None, "generic"),  # 64 tiles: too few
+    (2048, 2048, 30, None, None, None, "generic"),    # rows not 16-byte aligned
+    (1984, 2048, 32, None, None, None, "generic"),    # M not a multiple of 128
+])
+def test_fp32_gemm_kernels(device, m, n, k, lda, ldb, ldc, variant):
+    """fp32 on the fp32 MFMA kernel for whole 128 x 128 x 32 tiles and the
+    generic one otherwise, against fp64: every element within the fp32
+    accumulation bound K * 2^-24 * (|A||B|)_ij (deep K exceeds the reference's
+    1e-5 hybrid figure through summation alone: 2.8e-5 at K = 1024 on U[-1, 1]),
+    and the 1e-5 hybrid figure itself for K <= 256; C's padding columns stay
+    untouched."""
+    lda, ldb, ldc = lda or k, ldb or n, ldc or n
+    rng = np.random.default_rng(11)
+    a = rng.uniform(-1, 1, (m, lda)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, ldb)).astype(np.float32)
+    c, got = run_matmul(a.reshape(-1), b.reshape(-1), m, n, k, (lda, 1, ldb, 1, ldc, 1),
+                        c_elems=m * ldc, c_init=np.full(m * ldc, -7.0, np.float32))
+    assert got == f"tm_gemm_{variant}_f32"
+    c = c.reshape(m, ldc)
+    a64, b64 = a[:, :k].astype(np.float64), b[:, :n].astype(np.float64)
+    want = a64 @ b64
+    bound = k * 2.0 ** -24 * (np.abs(a64) @ np.abs(b64))
+    assert np.all(np.abs(c[:, :n] - want) <= bound)
+    if k <= 256:
+        assert T.hybrid_error(c[:, :n], want) <= 1e-5
+    assert np.all(c[:, n:] == -7.0)
 
 
 @pytest.mark.parametrize("element", ["bf16", "f16"])

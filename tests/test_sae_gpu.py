@@ -40,6 +40,7 @@ def encode(x, w, b, element="f32"):
     (64, 32, 64), (128, 128, 256), (64, 512, 2048),          # whole blocks (:44-50)
     (100, 300, 700), (1, 1, 1), (7, 13, 5), (65, 33, 65),     # ragged (:52-60)
     (1, 512, 4096),                                           # one token, wide dictionary (:62-68)
+    (2048, 256, 1024),                                        # 128 tiles: the fp32 MFMA kernel
 ])
 def test_f32_matches_the_oracle(device, rows, model, features):
     x, w, b = inputs(rows, model, features)

@@ -1,0 +1,173 @@
+/*
+ * Specialised gfx950 GEMM for fp32, the reference's own element type:
+ * C = A @ B with A [M, K], B [K, N], C [M, N] row-major (unit inner stride,
+ * 16-byte aligned rows, lda >= K, ldb >= N), M and N multiples of 128 and K a
+ * multiple of 32; fp32 products and accumulation on v_mfma_f32_16x16x4_f32
+ * (the reference's matmul_kernel semantics,
+ * Sources/TritonMetalBench/GEMMKernel.swift:28-174, in fp32).
+ *
+ * Tiling: one 256-thread workgroup (4 waves, 2 x 2) computes a 128 x 128
+ * tile of C; each wave a 64 x 64 sub-tile (4 x 4 accumulators of 16 x 16).
+ * Per K step of 32:
+ *   - A [128 x 32] and B [32 x 128] tiles are copied HBM -> LDS with
+ *     global_load_lds_dwordx4 in their row-major layouts (double buffered,
+ *     64 KB of LDS, two workgroups per CU), 16-byte chunks XOR-swizzled by row;
+ *   - the MFMA's k index is permuted within each 16-wide k chunk: lane
+ *     (g = l / 16, c = l % 16) feeds k = 4g + t to the t-th of four MFMAs, so
+ *     one ds_read_b128 of A row c supplies all four, and B's element
+ *     (k = 4g + t, column c) is one ds_read_b32;
+ *   - B is the MFMA's first operand, producing C^T tiles: each lane holds 4
+ *     consecutive columns of one row of C, stored as one 16-byte write.
+ */
+#include "common.h"
+
+namespace {
+
+constexpr int FT = 128, FK = 32;
+constexpr int FA_TILE = FT * FK * 4; /* 16 KB: 128 rows of 128 bytes */
+constexpr int FB_TILE = FK * FT * 4; /* 16 KB: 32 rows of 512 bytes */
+
+/* A tile: 128-byte rows, read by ds_read_b128 of 16 consecutive rows at one
+ * chunk: the key row & 7 spreads them over the banks. */
+TM_DEV int fa_off(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
+
+/* B tile: 512-byte rows; a wave reads rows 4g + t (g = 0..3) at 16
+ * consecutive floats (four chunks): the key 4 ((row >> 2) & 3) moves the four
+ * rows to different quarters of the 256-byte bank row. */
+TM_DEV int fb_off(int row, int chunk) { return row * 512 + ((chunk ^ (((row >> 2) & 3) << 2)) << 4); }
+
+TM_DEV void f_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+TM_DEV int f_xcd_remap(int wg, int nwg) {
+  const int q = nwg >> 3, r = nwg & 7;
+  const int xcd = wg & 7, slot = wg >> 3;
+  return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
+}
+
+/* A [128 x 32] tile at (m0, k0): 16 instructions of 8 rows, 4 per wave */
+TM_DEV void f_stage_a(const float *a, int64_t lda, int k0, char *tile, int wave, int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = wave * 4 + i;
+    const int row = t * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ (row & 7);
+    lds_copy16_global(a + (int64_t)row * lda + k0 + chunk * 4, lds_addr(tile + t * 1024));
+  }
+}
+
+/* B [32 x 128] tile at (k0, n0): 16 instructions of 2 rows, 4 per wave */
+TM_DEV void f_stage_b(const float *b, int64_t ldb, int k0, char *tile, int wave, int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = wave * 4 + i;
+    const int row = t * 2 + (lane >> 5);
+    const int chunk = (lane & 31) ^ (((row >> 2) & 3) << 2);
+    lds_copy16_global(b + (int64_t)(k0 + row) * ldb + chunk * 4, lds_addr(tile + t * 1024));
+  }
+}
+
+template <int EPI>
+TM_DEV void gemm_f32(const TmGemmArgs &p) {
+  __shared__ __align__(1024) char lds_a0[FA_TILE];
+  __shared__ __align__(1024) char lds_b0[FB_TILE];
+  __shared__ __align__(1024) char lds_a1[FA_TILE];
+  __shared__ __align__(1024) char lds_b1[FB_TILE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int wm = wave >> 1, wn = wave & 1; /* 2 x 2 waves */
+
+  /* tile order: XCD-contiguous ranges, walked in groups of 8 tile rows */
+  const int mt = p.m / FT, nt = p.n / FT;
+  const int logical = f_xcd_remap(blockIdx.x, gridDim.x);
+  constexpr int GROUP = 8;
+  const int per_group = GROUP * nt;
+  const int group = logical / per_group;
+  const int first_m = group * GROUP;
+  const int gm = min(mt - first_m, GROUP);
+  const int in_group = logical - group * per_group;
+  const int m0 = (first_m + in_group % gm) * FT, n0 = (in_group / gm) * FT;
+
+  const int64_t lda = p.sam, ldb = p.sbk, ldc = p.scm;
+  const float *A = (const float *)p.a + (int64_t)m0 * lda;
+  const float *B = (const float *)p.b + n0;
+  float *C = (float *)p.c;
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  const int ksteps = p.k / FK;
+  f_stage_a(A, lda, 0, lds_a0, wave, lane);
+  f_stage_b(B, ldb, 0, lds_b0, wave, lane);
+  f_wait_vmem();
+  __syncthreads();
+
+  auto step = [&](const char *ca, const char *cb, char *na, char *nb, int kb) {
+    if (kb + 1 < ksteps) {
+      f_stage_a(A, lda, (kb + 1) * FK, na, wave, lane);
+      f_stage_b(B, ldb, (kb + 1) * FK, nb, wave, lane);
+    }
+#pragma unroll
+    for (int kc = 0; kc < FK / 16; ++kc) {
+      /* B (first operand): element (k = 16 kc + 4g + t, column n) */
+      float bf[4][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = wn * 64 + j * 16 + c;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          bf[j][t] = *(const float *)(cb + fb_off(kc * 16 + 4 * g + t, n >> 2) + ((n & 3) << 2));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        /* A (second operand): row m, k = 16 kc + 4g .. +3 */
+        const f32x4 af = *(const f32x4 *)(ca + fa_off(wm * 64 + i * 16 + c, kc * 4 + g));
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = mfma_f32_16x16x4(bf[j][t], af[t], acc[i][j]);
+      }
+    }
+    f_wait_vmem();
+    __syncthreads();
+  };
+
+  for (int kb = 0; kb < ksteps; kb += 2) {
+    step(lds_a0, lds_b0, lds_a1, lds_b1, kb);
+    if (kb + 1 < ksteps) step(lds_a1, lds_b1, lds_a0, lds_b0, kb + 1);
+  }
+
+  /* acc[i][j] is the C^T tile: lane holds row m0 + wm*64 + i*16 + c,
+   * columns n0 + wn*64 + j*16 + 4g .. +3 */
+  f32x4 bias[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    bias[j] = EPI == EPI_BIAS_RELU
+                  ? *(const f32x4 *)((const float *)p.bias + n0 + wn * 64 + j * 16 + 4 * g)
+                  : (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + wm * 64 + i * 16 + c;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f32x4 v = acc[i][j];
+      if (EPI == EPI_BIAS_RELU) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = fmaxf(v[r] + bias[j][r], 0.f);
+      }
+      *(f32x4 *)(C + (int64_t)m * ldc + n0 + wn * 64 + j * 16 + 4 * g) = v;
+    }
+  }
+}
+
+} // namespace
+
+extern "C" __global__ __launch_bounds__(256) void tm_gemm_fast_f32(TmGemmArgs p) {
+  gemm_f32<EPI_NONE>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void tm_sae_fast_f32(TmGemmArgs p) {
+  gemm_f32<EPI_BIAS_RELU>(p);
+}
