@@ -211,6 +211,51 @@ def test_ragged_gemm(element, m, n, k, lda, ldb, ldc, device):
     assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)
 
 
+def _gemm_nt(m, n, k, element, lda=None, ldbt=None, ldc=None, seed=0):
+    """C = A B with B stored transposed (bt[n, k], row stride ldbt: the
+    x @ W^T layout); the padding columns of A and of B^T hold inf, and C is
+    fenced with -7 sentinels like _gemm's."""
+    lda, ldbt, ldc = lda or k, ldbt or k, ldc or n
+    rng = np.random.default_rng(seed)
+    a = round_to(rng.standard_normal((m, lda), dtype=np.float32), element)
+    bt = round_to(rng.standard_normal((n, ldbt), dtype=np.float32), element)
+    a[:, k:] = np.inf
+    bt[:, k:] = np.inf
+    dtype = DT[element]
+    A = DeviceBuffer.from_numpy(a, dtype)
+    B = DeviceBuffer.from_numpy(bt, dtype)
+    C = DeviceBuffer.from_numpy(np.full((m + 3, ldc), -7.0, np.float32), dtype)
+    kern = ops.library(element).kernels["matmul_kernel"]
+    try:
+        grid, kinds, values = ops.matmul_args(A, B, C, m, n, k, (lda, 1, 1, ldbt, ldc, 1))
+        _core.launch(kern, grid, 128, kinds, values)
+        variant = _core.kernel_variant(kern)
+        c = C.float32()
+    finally:
+        for x in (A, B, C):
+            x.free()
+    want = a[:, :k].astype(np.float64) @ bt[:, :k].astype(np.float64).T
+    return c, want, variant
+
+
+@pytest.mark.parametrize("element", ["bf16", "f16"])
+@pytest.mark.parametrize("m,n,k,lda,ldbt,ldc,kind", [
+    (256, 256, 64, None, None, None, "fast"),
+    (4096, 4096, 128, None, None, None, "fast"),
+    (129, 257, 65, 72, 72, 260, "ragged"),
+    (300, 1000, 136, None, None, None, "ragged"),
+    (4000, 4100, 200, 200, 208, 4100, "ragged"),
+])
+def test_transposed_b_gemm(element, m, n, k, lda, ldbt, ldc, kind, device):
+    """B stored transposed (stride_bk = 1) runs the specialised kernels too,
+    B's tile copied and read like A's."""
+    c, want, variant = _gemm_nt(m, n, k, element, lda, ldbt, ldc)
+    assert variant == f"tm_gemm_{kind}_nt{_tile_suffix(m, n)}_{element}"
+    assert np.all(np.isfinite(c[:m, :n]))
+    assert T.hybrid_error(c[:m, :n], want) <= 2e-2
+    assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)
+
+
 @pytest.mark.parametrize("m,n,k,lda,ldb,variant", [
     (256, 256, 60, None, None, "generic"),    # rows of A not 16-byte aligned
     (300, 200, 100, None, None, "generic"),

@@ -178,8 +178,12 @@ TM_DEV uint32_t g_pack2(float lo, float hi) {
 
 /* BM x BN tiles: 256 x 256 with 8 waves (2 x 4) of 128 x 64, or 128 x 128
  * with 4 waves (2 x 2) of 64 x 64 for problems with fewer 256 x 256 tiles
- * than compute units.  A wave's sub-tile is (BM / 2) x 64. */
-template <typename T, int EPI, bool RAGGED, int BM, int BN>
+ * than compute units.  A wave's sub-tile is (BM / 2) x 64.
+ * BT: B is stored transposed (element (k, n) at n * ldb + k, the layout of
+ * x @ W^T with W [N, K] row-major).  Its tile is then [BN x 64] k-contiguous
+ * like A's, copied and read the same way: the B operand is one
+ * ds_read_b128 instead of two transposed reads. */
+template <typename T, int EPI, bool RAGGED, int BM, int BN, bool BT = false>
 TM_DEV void gemm_fast(const TmGemmArgs &p) {
   typedef typename GVec8<T>::type v8;
   constexpr int GBM = BM, GBN = BN;
@@ -211,24 +215,27 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   const int tile_n = in_group / gm;
   const int m0 = tile_m * GBM, n0 = tile_n * GBN;
 
-  const int64_t lda = p.sam, ldb = p.sbk, ldc = p.scm;
+  const int64_t lda = p.sam, ldb = BT ? p.sbn : p.sbk, ldc = p.scm;
   const T *A = (const T *)p.a + (int64_t)m0 * lda;
-  const T *B = (const T *)p.b + n0;
+  const T *B = (const T *)p.b + (BT ? (int64_t)n0 * ldb : (int64_t)n0);
   T *C = (T *)p.c;
   const int a_rows = RAGGED ? min(p.m - m0, GBM) : GBM;
   const int b_cols = RAGGED ? min(p.n - n0, GBN) : GBN;
 
   const int va = a_lane_offset(lda, lane);
   int vb[4];
-  b_lane_offsets<BN>(ldb, wave, lane, vb);
+  if (BT) vb[0] = a_lane_offset(ldb, lane);
+  else b_lane_offsets<BN>(ldb, wave, lane, vb);
   auto stage = [&](char *ta, char *tb, int kb) {
     const int k0 = kb * GBK;
     if (RAGGED) {
       stage_a(A + k0, lda, a_rows, p.k - k0, va, ta, wave);
-      stage_b<T, BN>(B + (int64_t)k0 * ldb, ldb, p.k - k0, b_cols, vb, tb, wave);
+      if (BT) stage_a(B + k0, ldb, b_cols, p.k - k0, vb[0], tb, wave);
+      else stage_b<T, BN>(B + (int64_t)k0 * ldb, ldb, p.k - k0, b_cols, vb, tb, wave);
     } else {
       stage_a_global(A, lda, k0, ta, wave, lane);
-      stage_b_global<T, BN>(B, ldb, k0, tb, wave, lane);
+      if (BT) stage_a_global(B, ldb, k0, tb, wave, lane);
+      else stage_b_global<T, BN>(B, ldb, k0, tb, wave, lane);
     }
   };
 
@@ -243,8 +250,9 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   g_wait_vmem();
   __syncthreads();
 
-  /* LAST (ragged K only): A's k columns at or past K are zeroed in registers;
-   * B's rows past K were copied as zeros by the range check. */
+  /* LAST (ragged K only): A's k columns at or past K are zeroed in registers
+   * (and B's, when B is transposed); B's rows past K were copied as zeros by
+   * the range check. */
   auto step = [&](auto last_tag, const char *ca, const char *cb, char *na, char *nb, int kb) {
     constexpr bool LAST = decltype(last_tag)::value;
     if (!LAST && kb + 1 < ksteps) stage(na, nb, kb + 1);
@@ -252,8 +260,15 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
     for (int ks = 0; ks < 2; ++ks) {
       v8 bf[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bf[j] = __builtin_bit_cast(v8, read_b_operand<BN>(cb, ks * 32, wn * 64 + j * 16, g, c));
+      for (int j = 0; j < 4; ++j) {
+        if (BT) {
+          u32x4 b = *(const u32x4 *)(cb + a_off(wn * 64 + j * 16 + c, ks * 4 + g));
+          if (LAST) b = keep_first(b, p.k - kb * GBK - ks * 32 - 8 * g);
+          bf[j] = __builtin_bit_cast(v8, b);
+        } else {
+          bf[j] = __builtin_bit_cast(v8, read_b_operand<BN>(cb, ks * 32, wn * 64 + j * 16, g, c));
+        }
+      }
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         u32x4 a = *(const u32x4 *)(ca + a_off(wm * (BM / 2) + i * 16 + c, ks * 4 + g));
@@ -323,18 +338,22 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   }
 }
 
-#define TM_GEMM_ONE(NAME, T, EPI, RAGGED, TILE)                                             \
+#define TM_GEMM_ONE(NAME, T, EPI, RAGGED, TILE, BT)                                         \
   extern "C" __global__ __launch_bounds__(TILE * 2) void NAME(TmGemmArgs p) {                 \
-    gemm_fast<T, EPI, RAGGED, TILE, TILE>(p);                                                  \
+    gemm_fast<T, EPI, RAGGED, TILE, TILE, BT>(p);                                              \
   }
-#define TM_GEMM_FAST(T, TN)                                                 \
-  TM_GEMM_ONE(tm_gemm_fast_##TN, T, EPI_NONE, false, 256)                   \
-  TM_GEMM_ONE(tm_gemm_ragged_##TN, T, EPI_NONE, true, 256)                  \
-  TM_GEMM_ONE(tm_sae_fast_##TN, T, EPI_BIAS_RELU, false, 256)               \
-  TM_GEMM_ONE(tm_sae_ragged_##TN, T, EPI_BIAS_RELU, true, 256)              \
-  TM_GEMM_ONE(tm_gemm_fast_t128_##TN, T, EPI_NONE, false, 128)              \
-  TM_GEMM_ONE(tm_gemm_ragged_t128_##TN, T, EPI_NONE, true, 128)             \
-  TM_GEMM_ONE(tm_sae_fast_t128_##TN, T, EPI_BIAS_RELU, false, 128)          \
-  TM_GEMM_ONE(tm_sae_ragged_t128_##TN, T, EPI_BIAS_RELU, true, 128)
+#define TM_GEMM_FAST(T, TN)                                                     \
+  TM_GEMM_ONE(tm_gemm_fast_##TN, T, EPI_NONE, false, 256, false)                \
+  TM_GEMM_ONE(tm_gemm_ragged_##TN, T, EPI_NONE, true, 256, false)               \
+  TM_GEMM_ONE(tm_sae_fast_##TN, T, EPI_BIAS_RELU, false, 256, false)            \
+  TM_GEMM_ONE(tm_sae_ragged_##TN, T, EPI_BIAS_RELU, true, 256, false)           \
+  TM_GEMM_ONE(tm_gemm_fast_t128_##TN, T, EPI_NONE, false, 128, false)           \
+  TM_GEMM_ONE(tm_gemm_ragged_t128_##TN, T, EPI_NONE, true, 128, false)          \
+  TM_GEMM_ONE(tm_sae_fast_t128_##TN, T, EPI_BIAS_RELU, false, 128, false)       \
+  TM_GEMM_ONE(tm_sae_ragged_t128_##TN, T, EPI_BIAS_RELU, true, 128, false)      \
+  TM_GEMM_ONE(tm_gemm_fast_nt_##TN, T, EPI_NONE, false, 256, true)              \
+  TM_GEMM_ONE(tm_gemm_ragged_nt_##TN, T, EPI_NONE, true, 256, true)             \
+  TM_GEMM_ONE(tm_gemm_fast_nt_t128_##TN, T, EPI_NONE, false, 128, true)         \
+  TM_GEMM_ONE(tm_gemm_ragged_nt_t128_##TN, T, EPI_NONE, true, 128, true)
 TM_GEMM_FAST(bf16_t, bf16)
 TM_GEMM_FAST(f16_t, f16)
