@@ -256,6 +256,50 @@ def test_transposed_b_gemm(element, m, n, k, lda, ldbt, ldc, kind, device):
     assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)
 
 
+def _gemm_tn(m, n, k, element, ldat=None, ldb=None, ldc=None, seed=0):
+    """C = A B with A stored transposed (at[k, m], row stride ldat: the dY^T X
+    layout); A^T's padding columns hold inf, and C is fenced with -7."""
+    ldat, ldb, ldc = ldat or m, ldb or n, ldc or n
+    rng = np.random.default_rng(seed)
+    at = round_to(rng.standard_normal((k, ldat), dtype=np.float32), element)
+    b = round_to(rng.standard_normal((k, ldb), dtype=np.float32), element)
+    at[:, m:] = np.inf
+    b[:, n:] = np.nan
+    dtype = DT[element]
+    A = DeviceBuffer.from_numpy(at, dtype)
+    B = DeviceBuffer.from_numpy(b, dtype)
+    C = DeviceBuffer.from_numpy(np.full((m + 3, ldc), -7.0, np.float32), dtype)
+    kern = ops.library(element).kernels["matmul_kernel"]
+    try:
+        grid, kinds, values = ops.matmul_args(A, B, C, m, n, k, (1, ldat, ldb, 1, ldc, 1))
+        _core.launch(kern, grid, 128, kinds, values)
+        variant = _core.kernel_variant(kern)
+        c = C.float32()
+    finally:
+        for x in (A, B, C):
+            x.free()
+    want = at[:, :m].astype(np.float64).T @ b[:, :n].astype(np.float64)
+    return c, want, variant
+
+
+@pytest.mark.parametrize("element", ["bf16", "f16"])
+@pytest.mark.parametrize("m,n,k,ldat,ldb,ldc,kind", [
+    (256, 256, 64, None, None, None, "fast"),
+    (4096, 4096, 128, None, None, None, "fast"),
+    (129, 257, 65, 136, 264, 260, "ragged"),
+    (1000, 300, 136, None, 304, None, "ragged"),
+    (4100, 4000, 200, 4104, 4000, 4000, "ragged"),
+])
+def test_transposed_a_gemm(element, m, n, k, ldat, ldb, ldc, kind, device):
+    """A stored transposed (stride_am = 1) runs the specialised kernels too,
+    A's tile copied and read like B's."""
+    c, want, variant = _gemm_tn(m, n, k, element, ldat, ldb, ldc)
+    assert variant == f"tm_gemm_{kind}_tn{_tile_suffix(m, n)}_{element}"
+    assert np.all(np.isfinite(c[:m, :n]))
+    assert T.hybrid_error(c[:m, :n], want) <= 2e-2
+    assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)
+
+
 @pytest.mark.parametrize("m,n,k,lda,ldb,variant", [
     (256, 256, 60, None, None, "generic"),    # rows of A not 16-byte aligned
     (300, 200, 100, None, None, "generic"),

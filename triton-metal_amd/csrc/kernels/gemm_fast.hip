@@ -182,8 +182,11 @@ TM_DEV uint32_t g_pack2(float lo, float hi) {
  * BT: B is stored transposed (element (k, n) at n * ldb + k, the layout of
  * x @ W^T with W [N, K] row-major).  Its tile is then [BN x 64] k-contiguous
  * like A's, copied and read the same way: the B operand is one
- * ds_read_b128 instead of two transposed reads. */
-template <typename T, int EPI, bool RAGGED, int BM, int BN, bool BT = false>
+ * ds_read_b128 instead of two transposed reads.
+ * AT: A is stored transposed (element (m, k) at k * lda + m, the layout of
+ * dY^T X in a linear layer's weight gradient).  Its tile is then [64 x BM]
+ * m-contiguous like B's, copied and read the same way (transposed reads). */
+template <typename T, int EPI, bool RAGGED, int BM, int BN, bool BT = false, bool AT = false>
 TM_DEV void gemm_fast(const TmGemmArgs &p) {
   typedef typename GVec8<T>::type v8;
   constexpr int GBM = BM, GBN = BN;
@@ -215,25 +218,30 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   const int tile_n = in_group / gm;
   const int m0 = tile_m * GBM, n0 = tile_n * GBN;
 
-  const int64_t lda = p.sam, ldb = BT ? p.sbn : p.sbk, ldc = p.scm;
-  const T *A = (const T *)p.a + (int64_t)m0 * lda;
+  static_assert(!(AT && BT), "one transposed operand");
+  const int64_t lda = AT ? p.sak : p.sam, ldb = BT ? p.sbn : p.sbk, ldc = p.scm;
+  const T *A = (const T *)p.a + (AT ? (int64_t)m0 : (int64_t)m0 * lda);
   const T *B = (const T *)p.b + (BT ? (int64_t)n0 * ldb : (int64_t)n0);
   T *C = (T *)p.c;
   const int a_rows = RAGGED ? min(p.m - m0, GBM) : GBM;
   const int b_cols = RAGGED ? min(p.n - n0, GBN) : GBN;
 
-  const int va = a_lane_offset(lda, lane);
+  int va[4];
+  if (AT) b_lane_offsets<BM>(lda, wave, lane, va);
+  else va[0] = a_lane_offset(lda, lane);
   int vb[4];
   if (BT) vb[0] = a_lane_offset(ldb, lane);
   else b_lane_offsets<BN>(ldb, wave, lane, vb);
   auto stage = [&](char *ta, char *tb, int kb) {
     const int k0 = kb * GBK;
     if (RAGGED) {
-      stage_a(A + k0, lda, a_rows, p.k - k0, va, ta, wave);
+      if (AT) stage_b<T, BM>(A + (int64_t)k0 * lda, lda, p.k - k0, a_rows, va, ta, wave);
+      else stage_a(A + k0, lda, a_rows, p.k - k0, va[0], ta, wave);
       if (BT) stage_a(B + k0, ldb, b_cols, p.k - k0, vb[0], tb, wave);
       else stage_b<T, BN>(B + (int64_t)k0 * ldb, ldb, p.k - k0, b_cols, vb, tb, wave);
     } else {
-      stage_a_global(A, lda, k0, ta, wave, lane);
+      if (AT) stage_b_global<T, BM>(A, lda, k0, ta, wave, lane);
+      else stage_a_global(A, lda, k0, ta, wave, lane);
       if (BT) stage_a_global(B, ldb, k0, tb, wave, lane);
       else stage_b_global<T, BN>(B, ldb, k0, tb, wave, lane);
     }
@@ -271,8 +279,14 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
       }
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        u32x4 a = *(const u32x4 *)(ca + a_off(wm * (BM / 2) + i * 16 + c, ks * 4 + g));
-        if (LAST) a = keep_first(a, p.k - kb * GBK - ks * 32 - 8 * g);
+        u32x4 a;
+        if (AT) {
+          /* rows past K arrived as zeros */
+          a = read_b_operand<BM>(ca, ks * 32, wm * (BM / 2) + i * 16, g, c);
+        } else {
+          a = *(const u32x4 *)(ca + a_off(wm * (BM / 2) + i * 16 + c, ks * 4 + g));
+          if (LAST) a = keep_first(a, p.k - kb * GBK - ks * 32 - 8 * g);
+        }
         const v8 af = __builtin_bit_cast(v8, a);
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma_16x16x32(bf[j], af, acc[i][j]);
@@ -338,22 +352,26 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   }
 }
 
-#define TM_GEMM_ONE(NAME, T, EPI, RAGGED, TILE, BT)                                         \
+#define TM_GEMM_ONE(NAME, T, EPI, RAGGED, TILE, BT, AT)                                     \
   extern "C" __global__ __launch_bounds__(TILE * 2) void NAME(TmGemmArgs p) {                 \
-    gemm_fast<T, EPI, RAGGED, TILE, TILE, BT>(p);                                              \
+    gemm_fast<T, EPI, RAGGED, TILE, TILE, BT, AT>(p);                                          \
   }
-#define TM_GEMM_FAST(T, TN)                                                     \
-  TM_GEMM_ONE(tm_gemm_fast_##TN, T, EPI_NONE, false, 256, false)                \
-  TM_GEMM_ONE(tm_gemm_ragged_##TN, T, EPI_NONE, true, 256, false)               \
-  TM_GEMM_ONE(tm_sae_fast_##TN, T, EPI_BIAS_RELU, false, 256, false)            \
-  TM_GEMM_ONE(tm_sae_ragged_##TN, T, EPI_BIAS_RELU, true, 256, false)           \
-  TM_GEMM_ONE(tm_gemm_fast_t128_##TN, T, EPI_NONE, false, 128, false)           \
-  TM_GEMM_ONE(tm_gemm_ragged_t128_##TN, T, EPI_NONE, true, 128, false)          \
-  TM_GEMM_ONE(tm_sae_fast_t128_##TN, T, EPI_BIAS_RELU, false, 128, false)       \
-  TM_GEMM_ONE(tm_sae_ragged_t128_##TN, T, EPI_BIAS_RELU, true, 128, false)      \
-  TM_GEMM_ONE(tm_gemm_fast_nt_##TN, T, EPI_NONE, false, 256, true)              \
-  TM_GEMM_ONE(tm_gemm_ragged_nt_##TN, T, EPI_NONE, true, 256, true)             \
-  TM_GEMM_ONE(tm_gemm_fast_nt_t128_##TN, T, EPI_NONE, false, 128, true)         \
-  TM_GEMM_ONE(tm_gemm_ragged_nt_t128_##TN, T, EPI_NONE, true, 128, true)
+#define TM_GEMM_FAST(T, TN)                                                       \
+  TM_GEMM_ONE(tm_gemm_fast_##TN, T, EPI_NONE, false, 256, false, false)           \
+  TM_GEMM_ONE(tm_gemm_ragged_##TN, T, EPI_NONE, true, 256, false, false)          \
+  TM_GEMM_ONE(tm_sae_fast_##TN, T, EPI_BIAS_RELU, false, 256, false, false)       \
+  TM_GEMM_ONE(tm_sae_ragged_##TN, T, EPI_BIAS_RELU, true, 256, false, false)      \
+  TM_GEMM_ONE(tm_gemm_fast_t128_##TN, T, EPI_NONE, false, 128, false, false)      \
+  TM_GEMM_ONE(tm_gemm_ragged_t128_##TN, T, EPI_NONE, true, 128, false, false)     \
+  TM_GEMM_ONE(tm_sae_fast_t128_##TN, T, EPI_BIAS_RELU, false, 128, false, false)  \
+  TM_GEMM_ONE(tm_sae_ragged_t128_##TN, T, EPI_BIAS_RELU, true, 128, false, false) \
+  TM_GEMM_ONE(tm_gemm_fast_nt_##TN, T, EPI_NONE, false, 256, true, false)         \
+  TM_GEMM_ONE(tm_gemm_ragged_nt_##TN, T, EPI_NONE, true, 256, true, false)        \
+  TM_GEMM_ONE(tm_gemm_fast_nt_t128_##TN, T, EPI_NONE, false, 128, true, false)    \
+  TM_GEMM_ONE(tm_gemm_ragged_nt_t128_##TN, T, EPI_NONE, true, 128, true, false)   \
+  TM_GEMM_ONE(tm_gemm_fast_tn_##TN, T, EPI_NONE, false, 256, false, true)         \
+  TM_GEMM_ONE(tm_gemm_ragged_tn_##TN, T, EPI_NONE, true, 256, false, true)        \
+  TM_GEMM_ONE(tm_gemm_fast_tn_t128_##TN, T, EPI_NONE, false, 128, false, true)    \
+  TM_GEMM_ONE(tm_gemm_ragged_tn_t128_##TN, T, EPI_NONE, true, 128, false, true)
 TM_GEMM_FAST(bf16_t, bf16)
 TM_GEMM_FAST(f16_t, f16)

@@ -549,8 +549,9 @@ void validate_attn_common(const char *name, int64_t heads, int32_t stride_head,
  * and rows no shorter than the matrix (lda >= K, ldb >= N): whole tiles (and
  * K a multiple of 64) run the aligned kernel, any other M, N, K the ragged
  * one, whose copies clip at the matrix's last row and whose last k-step and
- * stores are masked; B may also be stored transposed (unit stride along K,
- * the x @ W^T layout), which the same kernels read like A.  fp32 with unit
+ * stores are masked.  Either operand (not both) may instead be stored
+ * transposed: B with unit stride along K (the x @ W^T layout), read like A,
+ * or A with unit stride along M (dY^T X), read like B.  fp32 with unit
  * inner strides, 16-byte aligned rows and
  * whole 128 x 128 x 32 tiles runs the fp32 MFMA kernel.  Anything else runs
  * the generic 64 x 64 kernel. */
@@ -569,15 +570,20 @@ void choose_gemm(Plan &plan, const TmGemmArgs &p, const BuiltinSpec &spec, const
     plan.block = 256;
     return;
   }
-  const bool half = fast_paths_enabled() && spec.element != Element::F32 && p.sak == 1 &&
-                    p.scn == 1 && p.k > 0 && p.sam % 8 == 0 && p.scm % 4 == 0 && p.sam >= p.k &&
-                    p.sam <= (1 << 26);
+  const bool half = fast_paths_enabled() && spec.element != Element::F32 && p.scn == 1 &&
+                    p.k > 0 && p.scm % 4 == 0;
+  const bool gemm = strcmp(family, "gemm") == 0;
+  /* A row-major [M, K], or (matmul only) stored transposed: element (m, k) at
+   * k * stride_ak + m, the dY^T X layout */
+  const bool a_n = half && p.sak == 1 && p.sam % 8 == 0 && p.sam >= p.k && p.sam <= (1 << 26);
+  const bool a_t = half && !a_n && gemm && p.sam == 1 && p.sak % 8 == 0 && p.sak >= p.m &&
+                   p.sak <= (1 << 26);
   /* B row-major [K, N], or (matmul only) stored transposed: element (k, n) at
    * n * stride_bn + k, the x @ W^T layout */
-  const bool nn = half && p.sbn == 1 && p.sbk % 8 == 0 && p.sbk >= p.n && p.sbk <= (1 << 26);
-  const bool nt = half && !nn && strcmp(family, "gemm") == 0 && p.sbk == 1 && p.sbn % 8 == 0 &&
-                  p.sbn >= p.k && p.sbn <= (1 << 26);
-  if (nn || nt) {
+  const bool b_n = p.sbn == 1 && p.sbk % 8 == 0 && p.sbk >= p.n && p.sbk <= (1 << 26);
+  const bool b_t = !b_n && gemm && p.sbk == 1 && p.sbn % 8 == 0 && p.sbn >= p.k && p.sbn <= (1 << 26);
+  const bool nn = a_n && b_n, nt = a_n && b_t, tn = a_t && b_n;
+  if (nn || nt || tn) {
     /* 256 x 256 tiles (512 threads, one resident per compute unit) or 128 x
      * 128 tiles (256 threads, two resident), whichever needs less time by
      * rounds of resident tiles: a round of 256 x 256 tiles takes about 31/21
@@ -589,8 +595,8 @@ void choose_gemm(Plan &plan, const TmGemmArgs &p, const BuiltinSpec &spec, const
                      cdiv(cdiv(p.m, 128) * cdiv(p.n, 128), 2 * cus) * 21;
     const int tile = big ? 256 : 128;
     const bool whole = p.m % tile == 0 && p.n % tile == 0 && p.k % 64 == 0;
-    plan.variant = format("tm_%s_%s%s%s_%s", family, whole ? "fast" : "ragged", nt ? "_nt" : "",
-                          big ? "" : "_t128", el);
+    plan.variant = format("tm_%s_%s%s%s_%s", family, whole ? "fast" : "ragged",
+                          nt ? "_nt" : tn ? "_tn" : "", big ? "" : "_t128", el);
     plan.grid[0] = (unsigned)(cdiv(p.m, tile) * cdiv(p.n, tile));
     plan.block = (unsigned)(2 * tile);
   } else {
