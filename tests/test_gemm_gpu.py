@@ -155,6 +155,22 @@ def test_config1_fp32_256_uniform(device):
     (1984, 2048, 32, None, None, None, "generic"),    # M not a multiple of 128
 ])
 def test_fp32_gemm_kernels(device, m, n, k, lda, ldb, ldc, variant):
+    _check_fp32_gemm(m, n, k, lda, ldb, ldc, variant, "nn")
+
+
+@pytest.mark.parametrize("layout", ["nt", "tn"])
+@pytest.mark.parametrize("m,n,k,ld_t,variant", [
+    (2048, 1024, 64, None, "fast"),
+    (1536, 2048, 96, 2052, "fast"),     # padded rows of the transposed operand
+    (1024, 1024, 256, None, "generic"),  # 64 tiles: too few
+])
+def test_fp32_transposed_operand(device, layout, m, n, k, ld_t, variant):
+    """One operand stored transposed: B with unit stride along K (nt) or A
+    with unit stride along M (tn)."""
+    _check_fp32_gemm(m, n, k, None, None, None, variant, layout, ld_t)
+
+
+def _check_fp32_gemm(m, n, k, lda, ldb, ldc, variant, layout, ld_t=None):
     """fp32 on the fp32 MFMA kernel for whole 128 x 128 x 32 tiles and the
     generic one otherwise, against fp64: every element within the fp32
     accumulation bound K * 2^-24 * (|A||B|)_ij (deep K exceeds the reference's
@@ -165,9 +181,21 @@ def test_fp32_gemm_kernels(device, m, n, k, lda, ldb, ldc, variant):
     rng = np.random.default_rng(11)
     a = rng.uniform(-1, 1, (m, lda)).astype(np.float32)
     b = rng.uniform(-1, 1, (k, ldb)).astype(np.float32)
-    c, got = run_matmul(a.reshape(-1), b.reshape(-1), m, n, k, (lda, 1, ldb, 1, ldc, 1),
+    a_flat, b_flat, strides = a.reshape(-1), b.reshape(-1), (lda, 1, ldb, 1, ldc, 1)
+    if layout == "nt":   # B^T [n, ld_t]
+        ld_t = ld_t or k
+        bt = np.full((n, ld_t), np.inf, np.float32)
+        bt[:, :k] = b[:, :n].T
+        b_flat, strides = bt.reshape(-1), (lda, 1, 1, ld_t, ldc, 1)
+    elif layout == "tn":  # A^T [k, ld_t]
+        ld_t = ld_t or m
+        at = np.full((k, ld_t), np.inf, np.float32)
+        at[:, :m] = a[:, :k].T
+        a_flat, strides = at.reshape(-1), (1, ld_t, ldb, 1, ldc, 1)
+    c, got = run_matmul(a_flat, b_flat, m, n, k, strides,
                         c_elems=m * ldc, c_init=np.full(m * ldc, -7.0, np.float32))
-    assert got == f"tm_gemm_{variant}_f32"
+    suffix = "" if layout == "nn" or variant == "generic" else "_" + layout
+    assert got == f"tm_gemm_{variant}{suffix}_f32"
     c = c.reshape(m, ldc)
     a64, b64 = a[:, :k].astype(np.float64), b[:, :n].astype(np.float64)
     want = a64 @ b64

@@ -18,6 +18,9 @@
  *     (k = 4g + t, column c) is one ds_read_b32;
  *   - B is the MFMA's first operand, producing C^T tiles: each lane holds 4
  *     consecutive columns of one row of C, stored as one 16-byte write.
+ * Either operand may instead be stored transposed (tm_gemm_fast_nt_f32: B
+ * with unit stride along K; tm_gemm_fast_tn_f32: A with unit stride along
+ * M); its tile then has the other operand's layout and reads.
  */
 #include "common.h"
 
@@ -66,8 +69,12 @@ TM_DEV void f_stage_b(const float *b, int64_t ldb, int k0, char *tile, int wave,
   }
 }
 
-template <int EPI>
+/* AT / BT: A (B) stored transposed -- element (m, k) at k * lda + m, or
+ * (k, n) at n * ldb + k.  A transposed operand's tile takes the other
+ * operand's layout and reads: A^T is staged and read like B, B^T like A. */
+template <int EPI, bool AT = false, bool BT = false>
 TM_DEV void gemm_f32(const TmGemmArgs &p) {
+  static_assert(!(AT && BT), "one transposed operand");
   __shared__ __align__(1024) char lds_a0[FA_TILE];
   __shared__ __align__(1024) char lds_b0[FB_TILE];
   __shared__ __align__(1024) char lds_a1[FA_TILE];
@@ -88,9 +95,15 @@ TM_DEV void gemm_f32(const TmGemmArgs &p) {
   const int in_group = logical - group * per_group;
   const int m0 = (first_m + in_group % gm) * FT, n0 = (in_group / gm) * FT;
 
-  const int64_t lda = p.sam, ldb = p.sbk, ldc = p.scm;
-  const float *A = (const float *)p.a + (int64_t)m0 * lda;
-  const float *B = (const float *)p.b + n0;
+  const int64_t lda = AT ? p.sak : p.sam, ldb = BT ? p.sbn : p.sbk, ldc = p.scm;
+  const float *A = (const float *)p.a + (AT ? (int64_t)m0 : (int64_t)m0 * lda);
+  const float *B = (const float *)p.b + (BT ? (int64_t)n0 * ldb : (int64_t)n0);
+  auto stage = [&](char *ta, char *tb, int k0) {
+    if (AT) f_stage_b(A, lda, k0, ta, wave, lane);
+    else f_stage_a(A + k0, lda, 0, ta, wave, lane);
+    if (BT) f_stage_a(B + k0, ldb, 0, tb, wave, lane);
+    else f_stage_b(B, ldb, k0, tb, wave, lane);
+  };
   float *C = (float *)p.c;
 
   f32x4 acc[4][4];
@@ -100,15 +113,13 @@ TM_DEV void gemm_f32(const TmGemmArgs &p) {
     for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   const int ksteps = p.k / FK;
-  f_stage_a(A, lda, 0, lds_a0, wave, lane);
-  f_stage_b(B, ldb, 0, lds_b0, wave, lane);
+  stage(lds_a0, lds_b0, 0);
   f_wait_vmem();
   __syncthreads();
 
   auto step = [&](const char *ca, const char *cb, char *na, char *nb, int kb) {
     if (kb + 1 < ksteps) {
-      f_stage_a(A, lda, (kb + 1) * FK, na, wave, lane);
-      f_stage_b(B, ldb, (kb + 1) * FK, nb, wave, lane);
+      stage(na, nb, (kb + 1) * FK);
     }
 #pragma unroll
     for (int kc = 0; kc < FK / 16; ++kc) {
@@ -117,14 +128,28 @@ TM_DEV void gemm_f32(const TmGemmArgs &p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int n = wn * 64 + j * 16 + c;
+        if (BT) {
+          const f32x4 v = *(const f32x4 *)(cb + fa_off(n, kc * 4 + g));
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-          bf[j][t] = *(const float *)(cb + fb_off(kc * 16 + 4 * g + t, n >> 2) + ((n & 3) << 2));
+          for (int t = 0; t < 4; ++t) bf[j][t] = v[t];
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            bf[j][t] = *(const float *)(cb + fb_off(kc * 16 + 4 * g + t, n >> 2) + ((n & 3) << 2));
+        }
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         /* A (second operand): row m, k = 16 kc + 4g .. +3 */
-        const f32x4 af = *(const f32x4 *)(ca + fa_off(wm * 64 + i * 16 + c, kc * 4 + g));
+        const int m = wm * 64 + i * 16 + c;
+        f32x4 af;
+        if (AT) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            af[t] = *(const float *)(ca + fb_off(kc * 16 + 4 * g + t, m >> 2) + ((m & 3) << 2));
+        } else {
+          af = *(const f32x4 *)(ca + fa_off(m, kc * 4 + g));
+        }
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -170,4 +195,10 @@ extern "C" __global__ __launch_bounds__(256) void tm_gemm_fast_f32(TmGemmArgs p)
 }
 extern "C" __global__ __launch_bounds__(256) void tm_sae_fast_f32(TmGemmArgs p) {
   gemm_f32<EPI_BIAS_RELU>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void tm_gemm_fast_nt_f32(TmGemmArgs p) {
+  gemm_f32<EPI_NONE, false, true>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void tm_gemm_fast_tn_f32(TmGemmArgs p) {
+  gemm_f32<EPI_NONE, true, false>(p);
 }

@@ -561,18 +561,24 @@ void choose_gemm(Plan &plan, const TmGemmArgs &p, const BuiltinSpec &spec, const
    * at least half as many tiles as compute units (fewer, larger problems
    * finish sooner on the generic kernel's 64 x 64 tiles: 1024^3 runs 53
    * TFLOP/s there against 29 on 64 tiles of 128 x 128; 2048^3 116 against 87) */
-  if (fast_paths_enabled() && spec.element == Element::F32 && p.sak == 1 && p.sbn == 1 &&
-      p.scn == 1 && p.m % 128 == 0 && p.n % 128 == 0 && p.k % 32 == 0 && p.k > 0 &&
-      2 * (int64_t)(p.m / 128) * (p.n / 128) >= std::max(device().compute_units, 1) &&
-      p.sam % 4 == 0 && p.sbk % 4 == 0 && p.scm % 4 == 0 && p.sam >= p.k && p.sbk >= p.n) {
-    plan.variant = format("tm_%s_fast_f32", family);
-    plan.grid[0] = (unsigned)((p.m / 128) * (p.n / 128));
-    plan.block = 256;
-    return;
+  const bool gemm = strcmp(family, "gemm") == 0;
+  if (fast_paths_enabled() && spec.element == Element::F32 && p.scn == 1 && p.m % 128 == 0 &&
+      p.n % 128 == 0 && p.k % 32 == 0 && p.k > 0 && p.scm % 4 == 0 &&
+      2 * (int64_t)(p.m / 128) * (p.n / 128) >= std::max(device().compute_units, 1)) {
+    /* either operand (matmul only, not both) may be stored transposed */
+    const bool a_n = p.sak == 1 && p.sam % 4 == 0 && p.sam >= p.k;
+    const bool a_t = gemm && !a_n && p.sam == 1 && p.sak % 4 == 0 && p.sak >= p.m;
+    const bool b_n = p.sbn == 1 && p.sbk % 4 == 0 && p.sbk >= p.n;
+    const bool b_t = gemm && !b_n && p.sbk == 1 && p.sbn % 4 == 0 && p.sbn >= p.k;
+    if ((a_n || a_t) && (b_n || b_t) && !(a_t && b_t)) {
+      plan.variant = format("tm_%s_fast%s_f32", family, b_t ? "_nt" : a_t ? "_tn" : "");
+      plan.grid[0] = (unsigned)((p.m / 128) * (p.n / 128));
+      plan.block = 256;
+      return;
+    }
   }
   const bool half = fast_paths_enabled() && spec.element != Element::F32 && p.scn == 1 &&
                     p.k > 0 && p.scm % 4 == 0;
-  const bool gemm = strcmp(family, "gemm") == 0;
   /* A row-major [M, K], or (matmul only) stored transposed: element (m, k) at
    * k * stride_ak + m, the dY^T X layout */
   const bool a_n = half && p.sak == 1 && p.sam % 8 == 0 && p.sam >= p.k && p.sam <= (1 << 26);
