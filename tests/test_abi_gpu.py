@@ -219,6 +219,52 @@ def test_extent_checks_do_not_wrap(core, device, builtin, args):
         core.release_library(lib)
 
 
+def test_concurrent_launches_from_several_threads(core, device):
+    """Threads sharing one library and kernel handle launch GEMMs on their own
+    buffers at once (tm_launch holds no caller state between calls): every
+    result is right and no handle leaks."""
+    import threading
+
+    from triton_metal import ops
+    from triton_metal.buffer import DeviceBuffer
+    kernel = ops.library("bf16").kernels["matmul_kernel"]
+    live = core.live_handle_count()
+    errors = []
+
+    def worker(seed):
+        try:
+            rng = np.random.default_rng(seed)
+            m, n, k = 256 + 64 * seed, 512, 128 + 32 * seed
+            a = rng.standard_normal((m, k), dtype=np.float32)
+            b = rng.standard_normal((k, n), dtype=np.float32)
+            A = DeviceBuffer.from_numpy(a, "bfloat16")
+            B = DeviceBuffer.from_numpy(b, "bfloat16")
+            C = DeviceBuffer((m, n), "bfloat16")
+            try:
+                a, b = A.float32(), B.float32()
+                for _ in range(5):
+                    grid, kinds, values = ops.matmul_args(A, B, C, m, n, k)
+                    core.launch(kernel, grid, 128, kinds, values)
+                    got = C.float32()
+                    want = a.astype(np.float64) @ b.astype(np.float64)
+                    err = np.max(np.abs(got - want) / np.maximum(1.0, np.abs(want)))
+                    if err > 2e-2:
+                        errors.append((seed, float(err)))
+            finally:
+                for x in (A, B, C):
+                    x.free()
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append((seed, repr(e)))
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(6)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert errors == []
+    assert core.live_handle_count() == live
+
+
 BLOCK_KERNEL = r"""
 #include <hip/hip_runtime.h>
 struct Block { const void *a, *b; void *c; int m, n, k, s0, s1, s2, s3, s4, s5; const void *bias; };
