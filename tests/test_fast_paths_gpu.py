@@ -300,6 +300,36 @@ def test_transposed_a_gemm(element, m, n, k, ldat, ldb, ldc, kind, device):
     assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)
 
 
+def _random_gemm_cases(count=36, seed=123):
+    """Seeded shapes for the layout sweep: M, N, K up to 700, each operand
+    row-major or (one of them) transposed, leading dimensions padded by 0-16
+    elements to a multiple of 8."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(count):
+        m, n, k = (int(x) for x in rng.integers(1, 700, 3))
+        layout = ("nn", "nt", "tn")[i % 3]
+        pad = lambda x: -(-(x + int(rng.integers(0, 17))) // 8) * 8
+        cases.append((m, n, k, layout, pad, ("bf16", "f16")[i % 2]))
+    return [(m, n, k, layout, pad(k), pad(n), pad(m), el) for m, n, k, layout, pad, el in cases]
+
+
+@pytest.mark.parametrize("m,n,k,layout,pk,pn,pm,element", _random_gemm_cases())
+def test_gemm_layout_sweep(m, n, k, layout, pk, pn, pm, element, device):
+    """Seeded random shapes and layouts through the specialised kernels,
+    each against fp64 with inf/NaN in every operand's padding."""
+    if layout == "nn":
+        c, want, variant = _gemm(m, n, k, element, pk, pn, pn, poison=True, extra_rows=3)
+    elif layout == "nt":
+        c, want, variant = _gemm_nt(m, n, k, element, pk, pk, pn)
+    else:
+        c, want, variant = _gemm_tn(m, n, k, element, pm, pn, pn)
+    assert "generic" not in variant, variant
+    assert np.all(np.isfinite(c[:m, :n]))
+    assert T.hybrid_error(c[:m, :n], want) <= 2e-2
+    assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)
+
+
 @pytest.mark.parametrize("m,n,k,lda,ldb,variant", [
     (256, 256, 60, None, None, "generic"),    # rows of A not 16-byte aligned
     (300, 200, 100, None, None, "generic"),
