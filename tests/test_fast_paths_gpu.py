@@ -103,6 +103,30 @@ def test_fast_attention_edges(element, dim, causal, seq, device):
     _check(out, dense, dim, causal)
 
 
+def _random_attention_cases(count=16, seed=7):
+    """Seeded sweep: sequence lengths up to 600, D 64 or 128, causal or not,
+    bf16 or f16, rows padded by 0-24 elements (kept 16-byte aligned) and a
+    head stride padded by 0-3 rows."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        seq = int(rng.integers(1, 600))
+        dim = (64, 128)[i % 2]
+        ss = dim + 8 * int(rng.integers(0, 4))
+        sh = (seq + int(rng.integers(0, 4))) * ss
+        out.append((int(rng.integers(1, 4)), seq, dim, ("bf16", "f16")[(i // 2) % 2], bool(i % 3 == 0),
+                    ss, sh))
+    return out
+
+
+@pytest.mark.parametrize("heads,seq,dim,element,causal,ss,sh", _random_attention_cases())
+def test_fast_attention_sweep(heads, seq, dim, element, causal, ss, sh, device):
+    out, variants, dense, _ = _attention(heads, seq, dim, element, causal, stride_seq=ss,
+                                         stride_head=sh, seed=seq)
+    assert all("_fast_" in v for v in variants), variants
+    _check(out, dense, dim, causal)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_fast_attention_padded_strides_leave_padding_untouched(causal, device):
     """Rows padded to stride_seq = D + 8 and heads to a padded stride_head: the
