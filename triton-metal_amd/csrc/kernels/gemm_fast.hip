@@ -1,21 +1,27 @@
 /*
  * Specialised gfx950 GEMM for 16-bit element types: C = A @ B with A [M, K],
- * B [K, N], C [M, N] row-major (unit inner stride, 16-byte aligned rows of A
- * and B, lda >= K, ldb >= N); f32 accumulation, output rounded to the element
- * type (the reference's matmul_kernel semantics,
- * Sources/TritonMetalBench/GEMMKernel.swift:28-174).  Two instantiations:
- * the aligned one for M and N multiples of 256 and K a multiple of 64, and
- * the ragged one for any other M, N, K, which masks its last k-step and its
- * stores.
+ * B [K, N], C [M, N] (unit inner stride, 16-byte aligned rows of A and B,
+ * rows no shorter than the matrix); f32 accumulation, output rounded to the
+ * element type (the reference's matmul_kernel semantics,
+ * Sources/TritonMetalBench/GEMMKernel.swift:28-174).  Instantiations:
+ *   - aligned (whole tiles, K a multiple of 64) or ragged (any M, N, K: the
+ *     copies clip at the matrix, the last k-step and the stores are masked);
+ *   - 256 x 256 tiles (512 threads) or 128 x 128 tiles ("t128", 256 threads,
+ *     for problems with too few large tiles to fill the chip);
+ *   - A and B row-major, or B stored transposed ("nt"), or A stored
+ *     transposed ("tn");
+ *   - plain, or with the SAE encoder's bias + ReLU epilogue (row-major only).
  *
- * Tiling: one 512-thread workgroup (8 waves, 2 x 4) computes a 256 x 256 tile
- * of C; each wave a 128 x 64 sub-tile on v_mfma_f32_16x16x32_{bf16,f16}
- * (8 x 4 accumulators of 16 x 16).  Per K step of 64:
+ * Tiling (256 x 256; the 128 x 128 tile halves every count): one 512-thread
+ * workgroup (8 waves, 2 x 4) computes a tile of C; each wave a 128 x 64
+ * sub-tile on v_mfma_f32_16x16x32_{bf16,f16} (8 x 4 accumulators of 16 x 16).
+ * Per K step of 64:
  *   - A [256 x 64] and B [64 x 256] tiles are copied HBM -> LDS with
- *     buffer_load ... lds (issued from inline assembly, so the compiler
- *     pipelines the operand reads behind it) in their natural row-major
- *     layouts (double buffered, 128 KB of LDS), 16-byte chunks XOR-swizzled
- *     by row; the buffer range check turns rows past the matrix into zeros;
+ *     global_load_lds_dwordx4 (aligned) or buffer_load ... lds (ragged: the
+ *     buffer range check turns rows past the matrix into zeros), issued from
+ *     inline assembly so the compiler pipelines the operand reads behind
+ *     them, in their natural row-major layouts (double buffered, 128 KB of
+ *     LDS), 16-byte chunks XOR-swizzled by row;
  *   - the A operand (row m, 8 consecutive k) is one ds_read_b128;
  *   - the B operand (column n, 8 consecutive k) is two ds_read_b64_tr_b16:
  *     lane i of a 16-lane group receives element (i & 3) of the 8 bytes
@@ -23,11 +29,14 @@
  *     columns n0 + 4q .. +3;
  *   - the MFMA takes B as its first operand, producing C^T tiles: each lane
  *     then holds 4 consecutive columns of one row, stored as one 8-byte write.
- * Ragged K: the last step's A fragments are zeroed past column K in
- * registers (the copies there read the next row, or the 16-byte rounding of
- * the last one), and B's rows past K arrive as zeros, so no value from outside
- * the matrices reaches a stored element.  Columns of B past N and rows of A
- * past M feed only the outputs past N and M, which are not stored.
+ * A transposed operand's tile has the other operand's layout and is copied
+ * and read the same way.
+ * Ragged K: the last step's k-contiguous fragments are zeroed past column K
+ * in registers (the copies there read the next row, or the 16-byte rounding
+ * of the last one), and k-major tiles' rows past K arrive as zeros, so no
+ * value from outside the matrices reaches a stored element.  Columns of B past
+ * N and rows of A past M feed only the outputs past N and M, which are not
+ * stored.
  * The 1-D grid is remapped so each XCD owns a contiguous range of tiles,
  * walked in groups of 8 tile rows so concurrently running tiles share A and B
  * panels in that XCD's L2.
