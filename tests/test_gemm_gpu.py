@@ -141,7 +141,7 @@ def test_config1_fp32_256_uniform(device):
     a = G.uniform((256, 256), seed=0)
     b = G.uniform((256, 256), seed=1)
     c, variant = run_matmul(a.reshape(-1), b.reshape(-1), 256, 256, 256, (256, 1, 256, 1, 256, 1))
-    assert variant == "tm_gemm_generic_f32"  # 4 tiles of 128 x 128: too few for the fp32 MFMA kernel
+    assert variant == "tm_gemm_fast_t64_f32"  # 16 tiles of 64 x 64
     want = a.astype(np.float64) @ b.astype(np.float64)
     assert T.hybrid_error(c.reshape(256, 256), want) <= 1e-5
 
@@ -150,9 +150,11 @@ def test_config1_fp32_256_uniform(device):
     (2048, 1024, 32, None, None, None, "fast"),      # 128 tiles: half the compute units
     (1536, 2048, 96, 100, 2052, 2056, "fast"),      # padded, 16-byte aligned rows
     (2048, 2048, 1024, None, None, None, "fast"),
-    (1024, 1024, 1024, None, None, None, "generic"),  # 64 tiles: too few
+    (1024, 1024, 1024, None, None, None, "fast_t64"),  # 64 tiles of 128: 64 x 64 tiles instead
+    (192, 320, 64, 196, 324, 324, "fast_t64"),
+    (160, 128, 32, None, None, None, "generic"),     # M not a multiple of 64
     (2048, 2048, 30, None, None, None, "generic"),    # rows not 16-byte aligned
-    (1984, 2048, 32, None, None, None, "generic"),    # M not a multiple of 128
+    (1984, 2048, 32, None, None, None, "fast_t64"),   # M a multiple of 64 only
 ])
 def test_fp32_gemm_kernels(device, m, n, k, lda, ldb, ldc, variant):
     _check_fp32_gemm(m, n, k, lda, ldb, ldc, variant, "nn")
@@ -162,7 +164,7 @@ def test_fp32_gemm_kernels(device, m, n, k, lda, ldb, ldc, variant):
 @pytest.mark.parametrize("m,n,k,ld_t,variant", [
     (2048, 1024, 64, None, "fast"),
     (1536, 2048, 96, 2052, "fast"),     # padded rows of the transposed operand
-    (1024, 1024, 256, None, "generic"),  # 64 tiles: too few
+    (1024, 1024, 256, None, "fast_t64"),  # 64 x 64 tiles
 ])
 def test_fp32_transposed_operand(device, layout, m, n, k, ld_t, variant):
     """One operand stored transposed: B with unit stride along K (nt) or A
@@ -194,8 +196,12 @@ def _check_fp32_gemm(m, n, k, lda, ldb, ldc, variant, layout, ld_t=None):
         a_flat, strides = at.reshape(-1), (1, ld_t, ldb, 1, ldc, 1)
     c, got = run_matmul(a_flat, b_flat, m, n, k, strides,
                         c_elems=m * ldc, c_init=np.full(m * ldc, -7.0, np.float32))
-    suffix = "" if layout == "nn" or variant == "generic" else "_" + layout
-    assert got == f"tm_gemm_{variant}{suffix}_f32"
+    if variant == "generic":
+        assert got == "tm_gemm_generic_f32"
+    else:
+        kind, _, tile = variant.partition("_")
+        suffix = ("" if layout == "nn" else "_" + layout) + ("_" + tile if tile else "")
+        assert got == f"tm_gemm_{kind}{suffix}_f32"
     c = c.reshape(m, ldc)
     a64, b64 = a[:, :k].astype(np.float64), b[:, :n].astype(np.float64)
     want = a64 @ b64

@@ -26,18 +26,18 @@
 
 namespace {
 
-constexpr int FT = 128, FK = 32;
-constexpr int FA_TILE = FT * FK * 4; /* 16 KB: 128 rows of 128 bytes */
-constexpr int FB_TILE = FK * FT * 4; /* 16 KB: 32 rows of 512 bytes */
+constexpr int FK = 32;
 
 /* A tile: 128-byte rows, read by ds_read_b128 of 16 consecutive rows at one
  * chunk: the key row & 7 spreads them over the banks. */
 TM_DEV int fa_off(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
 
-/* B tile: 512-byte rows; a wave reads rows 4g + t (g = 0..3) at 16
- * consecutive floats (four chunks): the key 4 ((row >> 2) & 3) moves the four
- * rows to different quarters of the 256-byte bank row. */
-TM_DEV int fb_off(int row, int chunk) { return row * 512 + ((chunk ^ (((row >> 2) & 3) << 2)) << 4); }
+/* B tile: FT-float rows (512 or 256 bytes); a wave reads rows 4g + t
+ * (g = 0..3) at 16 consecutive floats (four chunks): the key
+ * 4 ((row >> 2) & 3) moves the four rows to different quarters of the
+ * 256-byte bank row. */
+template <int FT>
+TM_DEV int fb_off(int row, int chunk) { return row * (4 * FT) + ((chunk ^ (((row >> 2) & 3) << 2)) << 4); }
 
 TM_DEV void f_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -47,24 +47,28 @@ TM_DEV int f_xcd_remap(int wg, int nwg) {
   return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
 }
 
-/* A [128 x 32] tile at (m0, k0): 16 instructions of 8 rows, 4 per wave */
+/* A [FT x 32] tile at (m0, k0): FT / 8 instructions of 8 rows over 4 waves */
+template <int FT>
 TM_DEV void f_stage_a(const float *a, int64_t lda, int k0, char *tile, int wave, int lane) {
+  constexpr int PER = FT / 32;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = wave * 4 + i;
+  for (int i = 0; i < PER; ++i) {
+    const int t = wave * PER + i;
     const int row = t * 8 + (lane >> 3);
     const int chunk = (lane & 7) ^ (row & 7);
     lds_copy16_global(a + (int64_t)row * lda + k0 + chunk * 4, lds_addr(tile + t * 1024));
   }
 }
 
-/* B [32 x 128] tile at (k0, n0): 16 instructions of 2 rows, 4 per wave */
+/* B [32 x FT] tile at (k0, n0): FT / 8 instructions of 256 / FT rows over 4 waves */
+template <int FT>
 TM_DEV void f_stage_b(const float *b, int64_t ldb, int k0, char *tile, int wave, int lane) {
+  constexpr int PER = FT / 32, RPI = 256 / FT, CPR = FT / 4;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = wave * 4 + i;
-    const int row = t * 2 + (lane >> 5);
-    const int chunk = (lane & 31) ^ (((row >> 2) & 3) << 2);
+  for (int i = 0; i < PER; ++i) {
+    const int t = wave * PER + i;
+    const int row = t * RPI + lane / CPR;
+    const int chunk = (lane % CPR) ^ (((row >> 2) & 3) << 2);
     lds_copy16_global(b + (int64_t)(k0 + row) * ldb + chunk * 4, lds_addr(tile + t * 1024));
   }
 }
@@ -72,9 +76,13 @@ TM_DEV void f_stage_b(const float *b, int64_t ldb, int k0, char *tile, int wave,
 /* AT / BT: A (B) stored transposed -- element (m, k) at k * lda + m, or
  * (k, n) at n * ldb + k.  A transposed operand's tile takes the other
  * operand's layout and reads: A^T is staged and read like B, B^T like A. */
-template <int EPI, bool AT = false, bool BT = false>
+template <int EPI, bool AT = false, bool BT = false, int FT = 128>
 TM_DEV void gemm_f32(const TmGemmArgs &p) {
   static_assert(!(AT && BT), "one transposed operand");
+  static_assert(FT == 128 || FT == 64, "tile");
+  constexpr int FA_TILE = FT * FK * 4; /* FT rows of 128 bytes */
+  constexpr int FB_TILE = FK * FT * 4; /* 32 rows of 4 FT bytes */
+  constexpr int WT = FT / 2, NI = WT / 16; /* a wave's sub-tile: WT x WT, NI x NI of 16 x 16 */
   __shared__ __align__(1024) char lds_a0[FA_TILE];
   __shared__ __align__(1024) char lds_b0[FB_TILE];
   __shared__ __align__(1024) char lds_a1[FA_TILE];
@@ -99,18 +107,18 @@ TM_DEV void gemm_f32(const TmGemmArgs &p) {
   const float *A = (const float *)p.a + (AT ? (int64_t)m0 : (int64_t)m0 * lda);
   const float *B = (const float *)p.b + (BT ? (int64_t)n0 * ldb : (int64_t)n0);
   auto stage = [&](char *ta, char *tb, int k0) {
-    if (AT) f_stage_b(A, lda, k0, ta, wave, lane);
-    else f_stage_a(A + k0, lda, 0, ta, wave, lane);
-    if (BT) f_stage_a(B + k0, ldb, 0, tb, wave, lane);
-    else f_stage_b(B, ldb, k0, tb, wave, lane);
+    if (AT) f_stage_b<FT>(A, lda, k0, ta, wave, lane);
+    else f_stage_a<FT>(A + k0, lda, 0, ta, wave, lane);
+    if (BT) f_stage_a<FT>(B + k0, ldb, 0, tb, wave, lane);
+    else f_stage_b<FT>(B, ldb, k0, tb, wave, lane);
   };
   float *C = (float *)p.c;
 
-  f32x4 acc[4][4];
+  f32x4 acc[NI][NI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NI; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   const int ksteps = p.k / FK;
   stage(lds_a0, lds_b0, 0);
@@ -124,10 +132,10 @@ TM_DEV void gemm_f32(const TmGemmArgs &p) {
 #pragma unroll
     for (int kc = 0; kc < FK / 16; ++kc) {
       /* B (first operand): element (k = 16 kc + 4g + t, column n) */
-      float bf[4][4];
+      float bf[NI][4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = wn * 64 + j * 16 + c;
+      for (int j = 0; j < NI; ++j) {
+        const int n = wn * WT + j * 16 + c;
         if (BT) {
           const f32x4 v = *(const f32x4 *)(cb + fa_off(n, kc * 4 + g));
 #pragma unroll
@@ -135,25 +143,25 @@ TM_DEV void gemm_f32(const TmGemmArgs &p) {
         } else {
 #pragma unroll
           for (int t = 0; t < 4; ++t)
-            bf[j][t] = *(const float *)(cb + fb_off(kc * 16 + 4 * g + t, n >> 2) + ((n & 3) << 2));
+            bf[j][t] = *(const float *)(cb + fb_off<FT>(kc * 16 + 4 * g + t, n >> 2) + ((n & 3) << 2));
         }
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < NI; ++i) {
         /* A (second operand): row m, k = 16 kc + 4g .. +3 */
-        const int m = wm * 64 + i * 16 + c;
+        const int m = wm * WT + i * 16 + c;
         f32x4 af;
         if (AT) {
 #pragma unroll
           for (int t = 0; t < 4; ++t)
-            af[t] = *(const float *)(ca + fb_off(kc * 16 + 4 * g + t, m >> 2) + ((m & 3) << 2));
+            af[t] = *(const float *)(ca + fb_off<FT>(kc * 16 + 4 * g + t, m >> 2) + ((m & 3) << 2));
         } else {
           af = *(const f32x4 *)(ca + fa_off(m, kc * 4 + g));
         }
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = mfma_f32_16x16x4(bf[j][t], af[t], acc[i][j]);
+          for (int j = 0; j < NI; ++j) acc[i][j] = mfma_f32_16x16x4(bf[j][t], af[t], acc[i][j]);
       }
     }
     f_wait_vmem();
@@ -165,25 +173,25 @@ TM_DEV void gemm_f32(const TmGemmArgs &p) {
     if (kb + 1 < ksteps) step(lds_a1, lds_b1, lds_a0, lds_b0, kb + 1);
   }
 
-  /* acc[i][j] is the C^T tile: lane holds row m0 + wm*64 + i*16 + c,
-   * columns n0 + wn*64 + j*16 + 4g .. +3 */
-  f32x4 bias[4];
+  /* acc[i][j] is the C^T tile: lane holds row m0 + wm*WT + i*16 + c,
+   * columns n0 + wn*WT + j*16 + 4g .. +3 */
+  f32x4 bias[NI];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < NI; ++j)
     bias[j] = EPI == EPI_BIAS_RELU
-                  ? *(const f32x4 *)((const float *)p.bias + n0 + wn * 64 + j * 16 + 4 * g)
+                  ? *(const f32x4 *)((const float *)p.bias + n0 + wn * WT + j * 16 + 4 * g)
                   : (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0 + wm * 64 + i * 16 + c;
+  for (int i = 0; i < NI; ++i) {
+    const int m = m0 + wm * WT + i * 16 + c;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NI; ++j) {
       f32x4 v = acc[i][j];
       if (EPI == EPI_BIAS_RELU) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[r] = fmaxf(v[r] + bias[j][r], 0.f);
       }
-      *(f32x4 *)(C + (int64_t)m * ldc + n0 + wn * 64 + j * 16 + 4 * g) = v;
+      *(f32x4 *)(C + (int64_t)m * ldc + n0 + wn * WT + j * 16 + 4 * g) = v;
     }
   }
 }
@@ -201,4 +209,17 @@ extern "C" __global__ __launch_bounds__(256) void tm_gemm_fast_nt_f32(TmGemmArgs
 }
 extern "C" __global__ __launch_bounds__(256) void tm_gemm_fast_tn_f32(TmGemmArgs p) {
   gemm_f32<EPI_NONE, true, false>(p);
+}
+/* 64 x 64 tiles (4 waves of 32 x 32) for problems with too few 128 x 128 tiles */
+extern "C" __global__ __launch_bounds__(256) void tm_gemm_fast_t64_f32(TmGemmArgs p) {
+  gemm_f32<EPI_NONE, false, false, 64>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void tm_sae_fast_t64_f32(TmGemmArgs p) {
+  gemm_f32<EPI_BIAS_RELU, false, false, 64>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void tm_gemm_fast_nt_t64_f32(TmGemmArgs p) {
+  gemm_f32<EPI_NONE, false, true, 64>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void tm_gemm_fast_tn_t64_f32(TmGemmArgs p) {
+  gemm_f32<EPI_NONE, true, false, 64>(p);
 }

@@ -551,28 +551,30 @@ void validate_attn_common(const char *name, int64_t heads, int32_t stride_head,
  * one, whose copies clip at the matrix's last row and whose last k-step and
  * stores are masked.  Either operand (not both) may instead be stored
  * transposed: B with unit stride along K (the x @ W^T layout), read like A,
- * or A with unit stride along M (dY^T X), read like B.  fp32 with unit
- * inner strides, 16-byte aligned rows and
- * whole 128 x 128 x 32 tiles runs the fp32 MFMA kernel.  Anything else runs
- * the generic 64 x 64 kernel. */
+ * or A with unit stride along M (dY^T X), read like B.  fp32 with the same
+ * layouts, 16-byte aligned rows and whole 128 x 128 (or, for problems with
+ * few of those, 64 x 64) x 32 tiles runs the fp32 MFMA kernel.  Anything else
+ * runs the generic 64 x 64 kernel. */
 void choose_gemm(Plan &plan, const TmGemmArgs &p, const BuiltinSpec &spec, const char *family) {
   const char *el = element_name(spec.element);
-  /* fp32: whole 128 x 128 x 32 tiles on the fp32 MFMA kernel, when there are
-   * at least half as many tiles as compute units (fewer, larger problems
-   * finish sooner on the generic kernel's 64 x 64 tiles: 1024^3 runs 53
-   * TFLOP/s there against 29 on 64 tiles of 128 x 128; 2048^3 116 against 87) */
+  /* fp32: whole 128 x 128 x 32 tiles on the fp32 MFMA kernel when there are
+   * at least half as many of them as compute units, else whole 64 x 64 tiles
+   * (1024^3 ran 29 TFLOP/s on 64 tiles of 128 x 128; 2048^3 runs 116) */
   const bool gemm = strcmp(family, "gemm") == 0;
-  if (fast_paths_enabled() && spec.element == Element::F32 && p.scn == 1 && p.m % 128 == 0 &&
-      p.n % 128 == 0 && p.k % 32 == 0 && p.k > 0 && p.scm % 4 == 0 &&
-      2 * (int64_t)(p.m / 128) * (p.n / 128) >= std::max(device().compute_units, 1)) {
+  const bool f32_big = p.m % 128 == 0 && p.n % 128 == 0 &&
+                       2 * (int64_t)(p.m / 128) * (p.n / 128) >= std::max(device().compute_units, 1);
+  if (fast_paths_enabled() && spec.element == Element::F32 && p.scn == 1 && p.m % 64 == 0 &&
+      p.n % 64 == 0 && p.k % 32 == 0 && p.k > 0 && p.scm % 4 == 0) {
     /* either operand (matmul only, not both) may be stored transposed */
     const bool a_n = p.sak == 1 && p.sam % 4 == 0 && p.sam >= p.k;
     const bool a_t = gemm && !a_n && p.sam == 1 && p.sak % 4 == 0 && p.sak >= p.m;
     const bool b_n = p.sbn == 1 && p.sbk % 4 == 0 && p.sbk >= p.n;
     const bool b_t = gemm && !b_n && p.sbk == 1 && p.sbn % 4 == 0 && p.sbn >= p.k;
     if ((a_n || a_t) && (b_n || b_t) && !(a_t && b_t)) {
-      plan.variant = format("tm_%s_fast%s_f32", family, b_t ? "_nt" : a_t ? "_tn" : "");
-      plan.grid[0] = (unsigned)((p.m / 128) * (p.n / 128));
+      const int tile = f32_big ? 128 : 64;
+      plan.variant = format("tm_%s_fast%s%s_f32", family, b_t ? "_nt" : a_t ? "_tn" : "",
+                            f32_big ? "" : "_t64");
+      plan.grid[0] = (unsigned)((p.m / tile) * (p.n / tile));
       plan.block = 256;
       return;
     }
