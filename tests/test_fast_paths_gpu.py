@@ -190,15 +190,20 @@ def _gemm(m, n, k, element, lda=None, ldb=None, ldc=None, seed=0, poison=False, 
 def _tile_suffix(m, n, cus=256):
     """The planner's tile choice on an MI355X (256 compute units): rounds of
     resident 256 x 256 tiles (one per CU) at 31 against rounds of 128 x 128
-    pairs (two per CU) at 21; "_t128" names the smaller tile."""
+    pairs (two per CU) at 21; with fewer 128 x 128 tiles than CUs, 64 x 64
+    tiles ("_t64")."""
     cd = lambda a, b: -(-a // b)
     big = cd(cd(m, 256) * cd(n, 256), cus) * 31 <= cd(cd(m, 128) * cd(n, 128), 2 * cus) * 21
-    return "" if big else "_t128"
+    if big:
+        return ""
+    return "_t64" if cd(m, 128) * cd(n, 128) < cus else "_t128"
 @pytest.mark.parametrize("element", ["bf16", "f16"])
 @pytest.mark.parametrize("m,n,k,lda,ldb,ldc,tile", [
-    (256, 512, 64, None, None, None, "_t128"),
-    (512, 256, 192, None, None, None, "_t128"),
-    (768, 1024, 320, 328, 1032, 1040, "_t128"),   # padded leading dimensions, 16-byte aligned
+    (256, 512, 64, None, None, None, "_t64"),
+    (512, 256, 192, None, None, None, "_t64"),
+    (768, 1024, 320, 328, 1032, 1040, "_t64"),    # padded leading dimensions, 16-byte aligned
+    (2048, 2048, 64, None, None, None, "_t128"),
+    (2560, 2048, 128, 136, 2056, 2052, "_t128"),
     (4096, 4096, 128, None, None, None, ""),
     (4096, 4096, 64, 72, 4104, 4100, ""),
 ])
@@ -222,6 +227,7 @@ def test_fast_gemm_shapes_and_strides(element, m, n, k, lda, ldb, ldc, tile, dev
     (513, 777, 1000, 1000, 784, 780),
     (4000, 4100, 200, 200, 4104, 4100),  # 272 tiles of 256 x 256
     (4096, 4096, 72, None, None, None),  # whole 256 x 256 tiles, ragged K
+    (2000, 2100, 72, None, 2104, 2100),  # 128 x 128 tiles
 ])
 def test_ragged_gemm(element, m, n, k, lda, ldb, ldc, device):
     """Any M, N, K with 16-byte aligned rows of A and B run the ragged
@@ -357,8 +363,10 @@ def test_gemm_layout_sweep(m, n, k, layout, pk, pn, pm, element, device):
 @pytest.mark.parametrize("m,n,k,lda,ldb,variant", [
     (256, 256, 60, None, None, "generic"),    # rows of A not 16-byte aligned
     (300, 200, 100, None, None, "generic"),
-    (255, 256, 64, None, None, "ragged_t128"),
-    (512, 256, 128, None, None, "fast_t128"),
+    (255, 256, 64, None, None, "ragged_t64"),
+    (512, 256, 128, None, None, "fast_t64"),
+    (2048, 2048, 64, None, None, "fast_t128"),
+    (2000, 2100, 72, None, 2104, "ragged_t128"),
     (4096, 4096, 64, None, None, "fast"),
 ])
 def test_gemm_kernel_choice(m, n, k, lda, ldb, variant, device):

@@ -111,10 +111,11 @@ def test_short_buffers_are_refused(device):
 
 @pytest.mark.parametrize("element", ["bf16", "f16"])
 @pytest.mark.parametrize("rows,model,features,variant", [
-    (512, 1024, 2048, "fast_t128"),  # whole 128 x 128 x 64 tiles
+    (512, 1024, 2048, "fast_t64"),   # whole 64 x 64 x 64 tiles
+    (2048, 1024, 2048, "fast_t128"), # whole 128 x 128 x 64 tiles
     (100, 300, 700, "generic"),      # rows not 16-byte aligned
-    (100, 512, 1000, "ragged_t128"), # M and N short of whole tiles
-    (333, 136, 264, "ragged_t128"),  # ragged K
+    (100, 512, 1000, "ragged_t64"),  # M and N short of whole tiles
+    (333, 136, 264, "ragged_t64"),   # ragged K
     (4096, 256, 4096, "fast"),       # 256 tiles of 256 x 256: one per compute unit
     (4000, 264, 4104, "ragged"),
 ])

@@ -70,9 +70,13 @@ TM_DEV int a_off(int row, int chunk) { return row * 128 + ((chunk ^ a_swz(row)) 
  * 256-byte bank width either way).  A transpose read touches rows
  * k0 + 8g + {0..3} (and +4) at one chunk pair; the even key separates the
  * pairs of the 8 rows served together. */
-TM_DEV int b_swz(int row) { return ((row & 3) | ((row >> 1) & 4)) << 1; }
 template <int BN>
-TM_DEV int b_off(int row, int chunk) { return row * (2 * BN) + ((chunk ^ b_swz(row)) << 4); }
+TM_DEV int b_swz(int row) {
+  /* 128-byte rows (BN = 64) have 8 chunks: the key keeps to 0..6 */
+  return BN >= 128 ? ((row & 3) | ((row >> 1) & 4)) << 1 : (row & 3) << 1;
+}
+template <int BN>
+TM_DEV int b_off(int row, int chunk) { return row * (2 * BN) + ((chunk ^ b_swz<BN>(row)) << 4); }
 
 /* Each copy instruction moves a few whole rows of a tile through a buffer
  * resource based at its first row, whose range ends at the matrix's last
@@ -124,7 +128,7 @@ TM_DEV void b_lane_offsets(int64_t ldb, int wave, int lane, int (&voff)[4]) {
   const int h = lane / CPR;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    voff[i] = h * (int)ldb * 2 + (((lane % CPR) ^ b_swz((wave * 4 + i) * RPI + h)) << 4);
+    voff[i] = h * (int)ldb * 2 + (((lane % CPR) ^ b_swz<BN>((wave * 4 + i) * RPI + h)) << 4);
 }
 
 /* The aligned kernel's copies: every row and column of a tile is inside the
@@ -150,7 +154,7 @@ TM_DEV void stage_b_global(const T *b, int64_t ldb, int k0, char *tile, int wave
   for (int i = 0; i < 4; ++i) {
     const int t = wave * 4 + i;
     const int row = t * RPI + lane / CPR;
-    const int chunk = (lane % CPR) ^ b_swz(row);
+    const int chunk = (lane % CPR) ^ b_swz<BN>(row);
     global_rows_to_lds(b + (int64_t)(k0 + row) * ldb + chunk * 8, tile + t * 1024);
   }
 }
@@ -203,7 +207,8 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   constexpr int B_TILE = GBK * BN * 2; /* 64 rows of 2 BN bytes */
   constexpr int WN = BN / 64;          /* waves across N */
   constexpr int MI = BM / 32;          /* 16-row tiles per wave */
-  static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 128), "tile shapes");
+  static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 128) || (BM == 64 && BN == 64),
+                "tile shapes");
   __shared__ __align__(1024) char lds_a0[A_TILE];
   __shared__ __align__(1024) char lds_b0[B_TILE];
   __shared__ __align__(1024) char lds_a1[A_TILE];
@@ -381,6 +386,14 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   TM_GEMM_ONE(tm_gemm_fast_tn_##TN, T, EPI_NONE, false, 256, false, true)         \
   TM_GEMM_ONE(tm_gemm_ragged_tn_##TN, T, EPI_NONE, true, 256, false, true)        \
   TM_GEMM_ONE(tm_gemm_fast_tn_t128_##TN, T, EPI_NONE, false, 128, false, true)    \
-  TM_GEMM_ONE(tm_gemm_ragged_tn_t128_##TN, T, EPI_NONE, true, 128, false, true)
+  TM_GEMM_ONE(tm_gemm_ragged_tn_t128_##TN, T, EPI_NONE, true, 128, false, true)   \
+  TM_GEMM_ONE(tm_gemm_fast_t64_##TN, T, EPI_NONE, false, 64, false, false)        \
+  TM_GEMM_ONE(tm_gemm_ragged_t64_##TN, T, EPI_NONE, true, 64, false, false)       \
+  TM_GEMM_ONE(tm_sae_fast_t64_##TN, T, EPI_BIAS_RELU, false, 64, false, false)    \
+  TM_GEMM_ONE(tm_sae_ragged_t64_##TN, T, EPI_BIAS_RELU, true, 64, false, false)   \
+  TM_GEMM_ONE(tm_gemm_fast_nt_t64_##TN, T, EPI_NONE, false, 64, true, false)      \
+  TM_GEMM_ONE(tm_gemm_ragged_nt_t64_##TN, T, EPI_NONE, true, 64, true, false)     \
+  TM_GEMM_ONE(tm_gemm_fast_tn_t64_##TN, T, EPI_NONE, false, 64, false, true)      \
+  TM_GEMM_ONE(tm_gemm_ragged_tn_t64_##TN, T, EPI_NONE, true, 64, false, true)
 TM_GEMM_FAST(bf16_t, bf16)
 TM_GEMM_FAST(f16_t, f16)

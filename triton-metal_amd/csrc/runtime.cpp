@@ -601,10 +601,13 @@ void choose_gemm(Plan &plan, const TmGemmArgs &p, const BuiltinSpec &spec, const
     const int64_t cus = std::max(device().compute_units, 1);
     const bool big = cdiv(cdiv(p.m, 256) * cdiv(p.n, 256), cus) * 31 <=
                      cdiv(cdiv(p.m, 128) * cdiv(p.n, 128), 2 * cus) * 21;
-    const int tile = big ? 256 : 128;
+    /* with fewer 128 x 128 tiles than compute units, 64 x 64 tiles (128
+     * threads): 1024^3 bf16 had 64 tiles of 128 x 128 */
+    const bool small = !big && cdiv(p.m, 128) * cdiv(p.n, 128) < cus;
+    const int tile = big ? 256 : small ? 64 : 128;
     const bool whole = p.m % tile == 0 && p.n % tile == 0 && p.k % 64 == 0;
     plan.variant = format("tm_%s_%s%s%s_%s", family, whole ? "fast" : "ragged",
-                          nt ? "_nt" : tn ? "_tn" : "", big ? "" : "_t128", el);
+                          nt ? "_nt" : tn ? "_tn" : "", big ? "" : small ? "_t64" : "_t128", el);
     plan.grid[0] = (unsigned)(cdiv(p.m, tile) * cdiv(p.n, tile));
     plan.block = (unsigned)(2 * tile);
   } else {
