@@ -6,13 +6,14 @@
  * Sources/TritonMetalBench/GEMMKernel.swift:28-174).  Instantiations:
  *   - aligned (whole tiles, K a multiple of 64) or ragged (any M, N, K: the
  *     copies clip at the matrix, the last k-step and the stores are masked);
- *   - 256 x 256 tiles (512 threads) or 128 x 128 tiles ("t128", 256 threads,
- *     for problems with too few large tiles to fill the chip);
+ *   - 256 x 256 tiles (512 threads), 128 x 128 tiles ("t128", 256 threads,
+ *     for problems with too few large tiles to fill the chip) or 64 x 64
+ *     tiles ("t64", 128 threads, for fewer 128 x 128 tiles than CUs);
  *   - A and B row-major, or B stored transposed ("nt"), or A stored
  *     transposed ("tn");
  *   - plain, or with the SAE encoder's bias + ReLU epilogue (row-major only).
  *
- * Tiling (256 x 256; the 128 x 128 tile halves every count): one 512-thread
+ * Tiling (256 x 256; each smaller tile halves every count): one 512-thread
  * workgroup (8 waves, 2 x 4) computes a tile of C; each wave a 128 x 64
  * sub-tile on v_mfma_f32_16x16x32_{bf16,f16} (8 x 4 accumulators of 16 x 16).
  * Per K step of 64:
@@ -189,9 +190,9 @@ TM_DEV uint32_t g_pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, t2));
 }
 
-/* BM x BN tiles: 256 x 256 with 8 waves (2 x 4) of 128 x 64, or 128 x 128
- * with 4 waves (2 x 2) of 64 x 64 for problems with fewer 256 x 256 tiles
- * than compute units.  A wave's sub-tile is (BM / 2) x 64.
+/* BM x BN tiles: 256 x 256 with 8 waves (2 x 4) of 128 x 64, 128 x 128 with
+ * 4 waves (2 x 2) of 64 x 64, or 64 x 64 with 2 waves (2 x 1) of 32 x 64.  A
+ * wave's sub-tile is (BM / 2) x 64.
  * BT: B is stored transposed (element (k, n) at n * ldb + k, the layout of
  * x @ W^T with W [N, K] row-major).  Its tile is then [BN x 64] k-contiguous
  * like A's, copied and read the same way: the B operand is one
