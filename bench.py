@@ -175,9 +175,12 @@ def bench_attention(core, ops, batch, heads, seq, dim, causal, steps, warmup, sa
     return wall_ms, per_kernel
 
 
-def bench_gemm(core, ops, n, warmup, sample_ms, element="bf16"):
+def bench_gemm(core, ops, n, warmup, sample_ms, element="bf16", layout="nn"):
+    """n^3 GEMM on N(0,1) operands.  layout "nt": B is passed transposed
+    (stride_bk = 1, the x @ W^T layout); "tn": A transposed (stride_am = 1)."""
     from triton_metal.buffer import DeviceBuffer, bf16_values
     dtype = {"bf16": "bfloat16", "f16": "float16", "f32": "float32"}[element]
+    strides = {"nn": (n, 1, n, 1, n, 1), "nt": (n, 1, 1, n, n, 1), "tn": (1, n, n, 1, n, 1)}[layout]
 
     def operand(seed):
         x = normal_bf16((n, n), seed)
@@ -187,7 +190,7 @@ def bench_gemm(core, ops, n, warmup, sample_ms, element="bf16"):
     c = DeviceBuffer((n, n), dtype)
     try:
         kernel = ops.library(element).kernels["matmul_kernel"]
-        grid, kinds, values = ops.matmul_args(a, b, c, n, n, n)
+        grid, kinds, values = ops.matmul_args(a, b, c, n, n, n, strides)
         for _ in range(warmup):
             core.launch_async(kernel, grid, 128, kinds, values)
         core.synchronize()
@@ -459,6 +462,14 @@ def main():
         components["gemm_f16_8192"] = {"tflops": round(tf16, 2),
                                        "frac_of_peak": round(tf16 / 2500, 4),
                                        "ms": round(ms16, 4), "variant": variant16}
+        # Other sizes and operand layouts on the same kernels (tile choice by size;
+        # B or A passed transposed).
+        more = {}
+        for n2, layout in ((1024, "nn"), (2048, "nn"), (4096, "nn"), (8192, "nt"), (8192, "tn")):
+            ms2, variant2 = bench_gemm(core, ops, n2, 2, args.sample_ms, layout=layout)
+            more[f"{layout}_{n2}"] = {"tflops": round(gemm_flops(n2, n2, n2) / (ms2 * 1e-3) / 1e12, 2),
+                                      "ms": round(ms2, 4), "variant": variant2}
+        components["gemm_bf16_sizes_and_layouts"] = more
         # The fused SAE encoder at an 8x dictionary over 8192 tokens of width 2048.
         rows, model, features = 8192, 2048, 16384
         ms_s, variant_s = bench_sae(core, ops, rows, model, features, args.warmup,
