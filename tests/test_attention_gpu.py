@@ -63,7 +63,7 @@ def test_forward_half_precision(device, heads, seq, dim, causal, element, tol):
         r.free()
     want_o, _, want_l = R.attention_forward(q, k, v, r.scale, causal)
     assert T.hybrid_error(o, want_o) <= tol
-    assert T.max_abs_error(lse, want_l) <= 2e-3
+    assert T.max_abs_error(lse, want_l) <= T.lse_bound(element)
 
 
 def test_forward_is_stable_on_scores_that_overflow_exp(device):
@@ -191,7 +191,7 @@ def test_forward_statistics_feed_the_backward(device, element, causal):
             _assert_within_bound(got, want[name], terms, T.U_F32,
                                  want["amplification"][name], name)
     else:
-        assert T.max_abs_error(lse, want["lse"]) <= 2e-3
+        assert T.max_abs_error(lse, want["lse"]) <= T.lse_bound(element)
         for name, got in (("dq", dq), ("dk", dk), ("dv", dv)):
             assert T.hybrid_error(got, want[name]) <= 2e-2, name
 

@@ -78,11 +78,11 @@ def _attention(heads, seq, dim, element, causal, stride_seq=None, stride_head=No
     return out, variants, dense, (total, sh, ss)
 
 
-def _check(out, dense, dim, causal, tol=2e-2):
+def _check(out, dense, dim, causal, tol=2e-2, element="bf16"):
     q, k, v, d_out = dense
     want = R.attention_backward(q, k, v, d_out, 1 / math.sqrt(dim), causal)
     assert T.max_abs_error(out["o"], want["o"]) <= tol
-    assert T.max_abs_error(out["lse"], want["lse"]) <= 2e-3
+    assert T.max_abs_error(out["lse"], want["lse"]) <= (2e-3 if element == "f32" else T.lse_bound(element))
     # Delta = rowsum(dO * O) over the O the forward wrote (already rounded to
     # the element type), in fp32: within the summation bound of D products
     o64, do64 = out["o"].astype(np.float64), d_out.astype(np.float64)
@@ -100,7 +100,7 @@ def _check(out, dense, dim, causal, tol=2e-2):
 def test_fast_attention_edges(element, dim, causal, seq, device):
     out, variants, dense, _ = _attention(2, seq, dim, element, causal)
     assert all("_fast_" in v for v in variants), variants
-    _check(out, dense, dim, causal)
+    _check(out, dense, dim, causal, element=element)
 
 
 def _random_attention_cases(count=16, seed=7):
@@ -124,7 +124,7 @@ def test_fast_attention_sweep(heads, seq, dim, element, causal, ss, sh, device):
     out, variants, dense, _ = _attention(heads, seq, dim, element, causal, stride_seq=ss,
                                          stride_head=sh, seed=seq)
     assert all("_fast_" in v for v in variants), variants
-    _check(out, dense, dim, causal)
+    _check(out, dense, dim, causal, element=element)
 
 
 @pytest.mark.parametrize("causal", [False, True])
@@ -155,7 +155,7 @@ def test_fast_attention_padded_strides_leave_padding_untouched(causal, device):
 def test_variant_selection(element, dim, stride_seq, expect, device):
     out, variants, dense, _ = _attention(1, 70, dim, element, False, stride_seq=stride_seq)
     assert all(f"_{expect}_" in v for v in variants), variants
-    _check(out, dense, dim, False, tol=2e-2 if element != "f32" else 1e-4)
+    _check(out, dense, dim, False, tol=2e-2 if element != "f32" else 1e-4, element=element)
 
 
 def _gemm(m, n, k, element, lda=None, ldb=None, ldc=None, seed=0, poison=False, extra_rows=0):

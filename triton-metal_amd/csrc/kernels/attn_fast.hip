@@ -1,18 +1,20 @@
 /*
  * Specialised gfx950 FlashAttention-2 kernels for 16-bit element types (bf16,
  * f16) at head_dim 64 and 128, contiguous head dimension, 16-byte aligned rows.
- * Same maths and numerics as the generic kernels (and the reference's
- * AttentionKernel.swift:40-250 / AttentionBackwardKernel.swift): f32 scores,
- * statistics and accumulators, P rounded to the element type before P V,
- * exp2 with sm_scale folded into log2(e), L = m + log2(l) in log2 units.
+ * Same maths as the generic kernels (and the reference's
+ * AttentionKernel.swift:40-250 / AttentionBackwardKernel.swift): f32 scores and
+ * accumulators, P rounded to the element type before P V, exp2 with sm_scale
+ * folded into log2(e), L = m + log2(l) in log2 units.  The forward's row sum l
+ * is the fp32 sum of the rounded P that P V uses (the reference sums the
+ * unrounded P; the two differ by at most the element type's rounding unit,
+ * relative).
  *
  * Forward tiling (one workgroup = 4 waves = 128 queries of one head):
  *   - each wave owns 32 queries, held in registers as the B operand of
  *     S^T = K Q^T on v_mfma_f32_16x16x32_{bf16,f16}: a lane then owns one query
- *     (column l%16) and 4 keys of every 16-key tile, so the row max needs only
- *     a reduction over the four 16-lane groups and the row sum none until the end;
+ *     (column l%16) and 4 keys of every 16-key tile;
  *   - O^T = V^T P^T keeps the lane <-> query ownership, so P goes from the
- *     softmax straight into the B operand and the rescale is lane-local;
+ *     softmax straight into the B operand; a ones tile beside V^T gives l;
  *   - K and V tiles [64 keys][D] are double-buffered in LDS in their natural
  *     row order, 16-byte chunks XOR-swizzled by row, each tile with the key
  *     that suits its reads; K feeds the A operand by ds_read_b128, V^T by the
@@ -28,6 +30,7 @@
 #include "common.h"
 
 #include <type_traits>
+#include <utility>
 
 #define TM_NEG_INF (-__builtin_inff())
 
@@ -160,25 +163,136 @@ TM_DEV u32x4 read_kmajor_operand(const char *tile, int r0, int d0, int g, int c)
 
 TM_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-/* ---- forward ------------------------------------------------------------- */
+/* ---- forward ----------------------------------------------------------------
+ * Software-pipelined over key blocks.  Iteration j of a wave issues the P V
+ * MFMAs of block j-1 and then the S MFMAs of block j+1, and in their shadow runs
+ * the softmax VALU work of block j: fma and exp2 of every score, the packing of
+ * P into the B operands of the next P V, and an OR over the packed words.  None
+ * of it depends on the MFMAs of the same iteration (the scores of block j
+ * completed during iteration j-1).  A gfx950 wave issues about two fp32 VALU
+ * operations (or one exp) in the shadow of each 16x16x32 MFMA; the softmax
+ * work is spread evenly over the iteration's MFMAs, with every dependent
+ * operation at least one MFMA after the one it waits for.
+ *
+ * Row sums come from the MFMA pipe: a seventeenth d tile whose A operand is all
+ * ones accumulates sum_k P[q][k] of the rounded P that the P V product uses, so
+ * O = acc / l is normalised by exactly the weights it was built from.
+ *
+ * Offsets: P = exp2(S * qk_scale - mb) with mb = m + B, m a running row maximum
+ * that moves only when it must (PBias below).  Block 0 sets m from its exact
+ * row maxima.
+ *
+ * LDS: K and V tiles double-buffered, in their natural row order with the
+ * 16-byte chunks XOR-swizzled (KEY_B128 for K, read by ds_read_b128; KEY_TR
+ * for V, read transposed).  Iteration j reads V(j-1) and K(j+1) and copies
+ * V(j) and K(j+2) into the buffers that V(j-2) and K(j) left; the copy
+ * instructions are spread over the MFMA stream (issued back to back they stall
+ * the wave on the memory pipeline for hundreds of cycles).
+ *
+ * The interleave is fixed with __builtin_amdgcn_sched_barrier fences between
+ * MFMAs and empty volatile asm "pins" on the VALU values, which keep the
+ * compiler from sinking each computation to its use or hoisting it to where
+ * its inputs become available. */
 
-/* Lazy-rescale threshold in log2 units (P <= 2^8 between rescales). */
-#define TM_RESCALE_THRESHOLD 8.0f
+template <typename F, int... I>
+TM_DEV void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+TM_DEV void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+template <int LO, typename F, int... I>
+TM_DEV void static_range_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, LO + I>{}), ...);
+}
+template <int LO, int HI, typename F>
+TM_DEV void static_range(F &&f) {
+  if constexpr (HI > LO) static_range_impl<LO>(f, std::make_integer_sequence<int, HI - LO>{});
+}
+#define TM_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+/* An empty volatile asm that reads and redefines a register: it emits nothing
+ * but keeps the value's computation on its side of the surrounding fences. */
+TM_DEV void pin(float &x) { asm volatile("" : "+v"(x)); }
+TM_DEV void pin(uint32_t &x) { asm volatile("" : "+v"(x)); }
+
+typedef __attribute__((address_space(3))) char lds_char_t;
+TM_DEV u32x4 lds_read16(uint32_t addr) {
+  return *(const __attribute__((address_space(3))) u32x4 *)(lds_char_t *)(uintptr_t)addr;
+}
+/* the two ds_read_b64_tr_b16 of a k-major operand (read_kmajor_operand) at LDS
+ * byte addresses base + off_a, base + off_b */
+TM_DEV u32x4 lds_read_kmajor(uint32_t base, int off_a, int off_b) {
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(lds_char_t *)(uintptr_t)(base + off_a));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(lds_char_t *)(uintptr_t)(base + off_b));
+  const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+  return (u32x4){ua[0], ua[1], ub[0], ub[1]};
+}
+
+/* Copies of [ROWS, D] tiles into XOR-swizzled LDS tiles (key KEY), the four
+ * waves sharing the work, one instruction at a time: the lane offsets are
+ * computed once; the buffer resource is based at the block's first row, so
+ * rows at or past n (and every row of a block at or past n) arrive as zeros. */
+template <typename T, int D, int ROWS, int KEY>
+struct TileCopy {
+  static constexpr int CPR = D / 8, RPI = 64 / CPR;     /* chunks per row, rows per instruction */
+  static constexpr int PER_WAVE = ROWS / RPI / 4;
+  static_assert(PER_WAVE >= 1 && ROWS % (RPI * 4) == 0, "tile rows");
+  int voff[PER_WAVE];
+  TM_DEV void init(int64_t ss, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const int row = (wave * PER_WAVE + i) * RPI + lane / CPR;
+      voff[i] = (int)(row * ss * 2) + (((lane % CPR) ^ swz<D, KEY>(row)) << 4);
+    }
+  }
+  static TM_DEV u32x4 rsrc(const T *src, int64_t ss, int k0, int n) {
+    const int64_t bytes = k0 < n ? (int64_t)(n - k0 - 1) * ss * 2 + D * 2 : 0;
+    return raw_buffer_rsrc(src + (int64_t)k0 * ss, bytes);
+  }
+  TM_DEV void issue(u32x4 rs, int i, uint32_t tile, int wave) const {
+    lds_copy16_buffer(rs, voff[i], tile + (uint32_t)((wave * PER_WAVE + i) * 1024));
+  }
+  TM_DEV void copy(const T *src, int64_t ss, int k0, int n, uint32_t tile, int wave) const {
+    const u32x4 rs = rsrc(src, ss, k0, n);
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) issue(rs, i, tile, wave);
+  }
+};
+
+/* Exponent bias of P.  P = exp2(S * qk_scale - m - B) keeps a row's values at
+ * or below 2^-B while its offset m is current, so the exponent field of every
+ * rounded P stays below the bit that marks 2.0 (bit 14 of a bf16 or an f16
+ * half), and an OR over the packed P words tells whether any value reached 2:
+ * a score more than B + 1 (log2 units) above the offset.  Only then does a
+ * block take its exact row maxima, move the offsets and redo its P.  bf16 has
+ * fp32's exponent range, so B = 32 lets the offset lag the maximum by 33 with
+ * no value near overflow; f16's range allows B = 2.  O = acc / l and
+ * L = mb + log2(l) are unchanged by any choice of offsets. */
+template <typename T> struct PBias;
+template <> struct PBias<bf16_t> { static constexpr float B = 32.f; };
+template <> struct PBias<f16_t> { static constexpr float B = 2.f; };
 
 template <typename T, int D, bool CAUSAL>
 TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
-  constexpr int BM = 128, BN = 64, QW = 32;
+  constexpr int QT = 2, BM = 128, QW = 32, BN = 64; /* query tiles per wave, queries per workgroup / wave, keys per block */
   constexpr int KS = D / 32;            /* k-steps of the S^T contraction */
-  constexpr int TILE = BN * D * 2;      /* bytes of one K or V tile */
-  /* Two separate arrays (not one [2][...]) so the compiler can tell the
-   * prefetch's LDS writes from the current tile's reads and does not wait for
-   * the prefetch before reading. */
-  __shared__ __align__(1024) char lds_a[2 * TILE];
-  __shared__ __align__(1024) char lds_b[2 * TILE];
+  constexpr int DT = D / 16;            /* 16-wide d tiles of O^T */
+  constexpr int TILE = BN * D * 2;
+  constexpr int NM1 = 4 * KS * QT;      /* S MFMAs per block */
+  constexpr int NM2 = (DT + 1) * 2 * QT; /* P V MFMAs per block, row sums included */
+  constexpr int VS = QT * 32;           /* softmax slots per iteration (4 per element pair) */
+  constexpr int LA = 2;                 /* operands read ahead */
+  constexpr float BIAS = PBias<T>::B;
+  __shared__ __align__(1024) char lds[4 * TILE];
+  const uint32_t kb0 = lds_addr(lds), kb1 = kb0 + TILE, vb0 = kb0 + 2 * TILE, vb1 = kb0 + 3 * TILE;
 
   typedef typename Vec8<T>::type v8;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); /* uniform: LDS bases are scalar */
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
   const int n = p.n_ctx;
   const int nqb = (n + BM - 1) / BM;
@@ -197,155 +311,292 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
 
   const int kend = CAUSAL ? min(n, q0 + BM) : n;
   const int nblocks = (kend + BN - 1) / BN;
-  if (nblocks > 0) {
-    stage_rows<T, D, BN, KEY_B128>(Kg, ss, 0, n, lds_a, wave, lane);
-    stage_rows<T, D, BN>(Vg, ss, 0, n, lds_a + TILE, wave, lane);
-  }
+  /* blocks [0, first_edge) need no mask */
+  const int first_edge = CAUSAL ? min(q0 / BN, n / BN) : n / BN;
 
-  /* Q fragments (B operand): query qw0 + qt*16 + c, d = ks*32 + 8g .. +7. */
-  u32x4 qf[2][KS];
+  TileCopy<T, D, BN, KEY_B128> kcp;
+  TileCopy<T, D, BN, KEY_TR> vcp;
+  kcp.init(ss, wave, lane);
+  vcp.init(ss, wave, lane);
+  if (nblocks > 0) kcp.copy(Kg, ss, 0, n, kb0, wave);
+  if (nblocks > 1) kcp.copy(Kg, ss, BN, n, kb1, wave);
+  u32x4 qf[QT][KS];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     const int qi = min(qw0 + qt * 16 + c, n - 1);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       qf[qt][ks] = *(const u32x4 *)(Qg + (int64_t)qi * ss + ks * 32 + 8 * g);
   }
-
+  /* lane parts of the operand addresses: K fragment (row c, k-step ks) and
+   * V^T fragment (d tile dt); the row offsets of kt, kk and the second
+   * transposed read are immediates */
+  uint32_t koff[KS], voff[DT];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = (uint32_t)tile_off<D, KEY_B128>(c, ks * 4 + g);
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+    voff[dt] = (uint32_t)(tile_off<D>(4 * g + (c >> 2), 2 * dt + ((c & 3) >> 1)) + ((c & 1) << 3));
+  /* the A operand of the row-sum MFMAs: sixteen rows of ones */
+  const uint32_t one2 = pack2<T>(1.f, 1.f);
+  const u32x4 ones = (u32x4){one2, one2, one2, one2};
   const float qk_scale = p.sm_scale * TM_LOG2E;
-  float m_i[2] = {TM_NEG_INF, TM_NEG_INF};
-  float l_i[2] = {0.f, 0.f}; /* per-lane partial sums over this lane's keys */
-  f32x4 acc[D / 16][2];
+  float mb[QT];                 /* offsets m + B */
+  f32x4 acc[DT + 1][QT];        /* O^T tiles, then the row sums (four equal rows) */
 #pragma unroll
-  for (int dt = 0; dt < D / 16; ++dt) acc[dt][0] = acc[dt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int dt = 0; dt <= DT; ++dt)
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) acc[dt][qt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  /* scores of the block whose softmax runs next and the packed P^T B operands
+   * [qt][kk] of the block whose P V runs next, each in two sets that the
+   * iterations of the interior loop alternate */
+  f32x4 s[4][QT], s2[4][QT];
+  u32x4 pf[QT][2], pf2[QT][2];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) pf[qt][0] = pf[qt][1] = (u32x4){0u, 0u, 0u, 0u};
 
-  wait_vmem();
-  __syncthreads();
-
-  /* One key block: prefetch block j+1 into `nxt`, compute block j from `cur`.
-   * EDGE blocks (the causal diagonal band, a ragged end) apply the mask;
-   * interior blocks are straight-line code. */
-  auto step = [&](auto edge_tag, const char *cur, char *nxt, int j) {
-    constexpr bool EDGE = decltype(edge_tag)::value;
-    const int k0 = j * BN;
-    if (j + 1 < nblocks) {
-      stage_rows<T, D, BN, KEY_B128>(Kg, ss, k0 + BN, n, nxt, wave, lane);
-      stage_rows<T, D, BN>(Vg, ss, k0 + BN, n, nxt + TILE, wave, lane);
-    }
-    /* S^T = K Q^T: 4 key tiles x 2 query tiles */
-    f32x4 s[4][2];
+  auto mask_block = [&](f32x4 (&sc)[4][QT], int k0) {
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      s[kt][0] = s[kt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const v8 a = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D, KEY_B128>(kt * 16 + c, ks * 4 + g)));
-        s[kt][0] = mfma_16x16x32(a, as_vec8<T>(qf[0][ks]), s[kt][0]);
-        s[kt][1] = mfma_16x16x32(a, as_vec8<T>(qf[1][ks]), s[kt][1]);
-      }
-    }
-    u32x4 pf[2][2]; /* P^T B operand: [query tile][key k-step] */
-    float mxs[2];
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      if (EDGE) {
-        const int qi = qw0 + qt * 16 + c;
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = k0 + kt * 16 + 4 * g + r;
-            s[kt][qt][r] = (key >= n || (CAUSAL && key > qi)) ? TM_NEG_INF : s[kt][qt][r];
-          }
-      }
-      float mx = vmax(s[0][qt][0], s[0][qt][1]);
-#pragma unroll
-      for (int e = 2; e < 16; e += 2)
-        mx = vmax(vmax(mx, s[e >> 2][qt][e & 3]), s[e >> 2][qt][(e & 3) + 1]);
-      mxs[qt] = group4_max(mx) * qk_scale;
-    }
-    /* Lazy rescale: a row's exponent offset m only moves when the block max
-     * exceeds it by more than TM_RESCALE_THRESHOLD (P then stays below 2^8).
-     * The final O = acc / l and L = m + log2(l) use the same m, so this is the
-     * same softmax; the O rescale (64 multiplies) runs only when some lane of
-     * the wave needs it. */
-    if (__builtin_amdgcn_ballot_w64(mxs[0] > m_i[0] + TM_RESCALE_THRESHOLD ||
-                                    mxs[1] > m_i[1] + TM_RESCALE_THRESHOLD) != 0) {
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        const float m_new = fmaxf(m_i[qt], mxs[qt]);
-        const float alpha = fast_exp2(m_i[qt] - m_new);
-        m_i[qt] = m_new;
-        l_i[qt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) acc[dt][qt] *= alpha;
-      }
-    }
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      float pv[4][4];
+    for (int qt = 0; qt < QT; ++qt) {
+      const int qi = qw0 + qt * 16 + c;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          pv[kt][r] = fast_exp2(__builtin_fmaf(s[kt][qt][r], qk_scale, -m_i[qt]));
-      float rs = pv[0][0];
+        for (int r = 0; r < 4; ++r) {
+          const int key = k0 + kt * 16 + 4 * g + r;
+          sc[kt][qt][r] = (key >= n || (CAUSAL && key > qi)) ? TM_NEG_INF : sc[kt][qt][r];
+        }
+    }
+  };
+  /* exact row maxima of a block times qk_scale, reduced over the 4 lane groups */
+  auto row_max = [&](const f32x4 (&sc)[4][QT], float (&out)[QT]) {
 #pragma unroll
-      for (int e = 1; e < 16; ++e) rs += pv[e >> 2][e & 3];
-      l_i[qt] += rs;
+    for (int qt = 0; qt < QT; ++qt) {
+      float mx = vmax(sc[0][qt][0], sc[0][qt][1]);
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        pf[qt][kk][0] = pack2<T>(pv[2 * kk][0], pv[2 * kk][1]);
-        pf[qt][kk][1] = pack2<T>(pv[2 * kk][2], pv[2 * kk][3]);
-        pf[qt][kk][2] = pack2<T>(pv[2 * kk + 1][0], pv[2 * kk + 1][1]);
-        pf[qt][kk][3] = pack2<T>(pv[2 * kk + 1][2], pv[2 * kk + 1][3]);
+      for (int e = 2; e < 16; e += 2)
+        mx = vmax(vmax(mx, sc[e >> 2][qt][e & 3]), sc[e >> 2][qt][(e & 3) + 1]);
+      out[qt] = group4_max(mx) * qk_scale;
+    }
+  };
+  /* S^T of one block from K fragments read by `kfrag(kt, ks)` */
+  auto scores = [&](f32x4 (&sc)[4][QT], auto kfrag) {
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) sc[kt][qt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const v8 a = as_vec8<T>(kfrag(kt, ks));
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) sc[kt][qt] = mfma_16x16x32(a, as_vec8<T>(qf[qt][ks]), sc[kt][qt]);
       }
     }
-    /* O^T += V^T P^T */
-    const char *vt = cur + TILE;
+  };
+
+  wait_vmem();
+  __syncthreads();
+  if (nblocks == 0) return;
+
+  /* block 0: scores, and the offsets from its exact row maxima */
+  scores(s, [&](int kt, int ks) { return lds_read16(kb0 + koff[ks] + kt * 16 * D * 2); });
+  if (first_edge == 0) mask_block(s, 0);
+  {
+    float mx[QT];
+    row_max(s, mx);
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
+    for (int qt = 0; qt < QT; ++qt) mb[qt] = mx[qt] + BIAS;
+  }
+  /* every wave has read kb0 before iteration 0 copies K(2) into it */
+  __syncthreads();
+
+  /* Iteration j.  PV: the P V of block j-1; SM: the softmax of block j; SN: the
+   * scores of block j+1 (the tail computes them even for a block that does not
+   * exist, from stale LDS; they are never used); EDGE: block j takes the mask.
+   * vrd/krd: LDS addresses of the V(j-1) and K(j+1) tiles; vdst/kdst: where
+   * V(j) and K(j+2) are copied. */
+  auto iteration = [&](auto pv_tag, auto sm_tag, auto sn_tag, auto edge_tag, uint32_t vrd,
+                       uint32_t krd, uint32_t vdst, uint32_t kdst, int j, f32x4 (&s)[4][QT],
+                       f32x4 (&sn)[4][QT], u32x4 (&pf)[QT][2], u32x4 (&pn)[QT][2]) {
+    constexpr bool PV = decltype(pv_tag)::value;
+    constexpr bool SM = decltype(sm_tag)::value;
+    constexpr bool SN = decltype(sn_tag)::value;
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    constexpr int NA = PV ? NM2 : 0, NB = SN ? NM1 : 0, NM = NA + NB;
+    const int k0 = j * BN;
+    /* copies of V(j) and K(j+2), one instruction every CSTRIDE MFMAs (a K
+     * block past the end copies zeros) */
+    constexpr int NCV = SM ? decltype(vcp)::PER_WAVE : 0, NCK = decltype(kcp)::PER_WAVE;
+    constexpr int NC = NCV + NCK;
+    constexpr int CSTRIDE = NM >= 4 * NC ? 4 : (NM >= 2 * NC ? 2 : 1);
+    const u32x4 rsv = decltype(vcp)::rsrc(Vg, ss, k0, n);
+    const u32x4 rsk = decltype(kcp)::rsrc(Kg, ss, k0 + 2 * BN, n);
+    auto copy_at = [&](auto cc) {
+      constexpr int cidx = decltype(cc)::value;
+      if constexpr (cidx < NCV) vcp.issue(rsv, cidx, vdst, wave);
+      else if constexpr (cidx < NC) kcp.issue(rsk, cidx - NCV, kdst, wave);
+    };
+
+    /* operand o: (kk, dt) of the P V part for o < NA/QT, the row-sum ones
+     * first in each kk (no LDS wait behind them), then (kt, ks) of the S part */
+    u32x4 opnd[NM > 0 ? NM / QT : 1];
+    auto read_op = [&](auto oo) {
+      constexpr int o = decltype(oo)::value;
+      if constexpr (o < NA / QT) {
+        constexpr int kk = o / (DT + 1), dt = (o % (DT + 1) + DT) % (DT + 1);
+        if constexpr (dt == DT) opnd[o] = ones;
+        else opnd[o] = lds_read_kmajor(vrd + voff[dt], 32 * kk * D * 2, (32 * kk + 16) * D * 2);
+      } else if constexpr (o < NM / QT) {
+        constexpr int b = o - NA / QT, kt = b / KS, ks = b % KS;
+        opnd[o] = lds_read16(krd + koff[ks] + kt * 16 * D * 2);
+      }
+    };
+    /* softmax slot v: element pair u = v / 4 (elements 2w, 2w+1 of [qt][kk])
+     * as fma, exp, pack and OR on four consecutive slots */
+    uint32_t big = 0;       /* OR of the packed P words */
+    float px[2], pe[2];
+    uint32_t wd = 0;
+    auto vslot = [&](auto vv) {
+      constexpr int v = decltype(vv)::value;
+      constexpr int u = v / 4, beat = v % 4, qt = u / 8, kk = (u / 4) % 2, w = u % 4;
+      constexpr int e0 = 2 * w, e1 = 2 * w + 1;
+      if constexpr (beat == 0) {
+        px[0] = __builtin_fmaf(s[2 * kk + (e0 >> 2)][qt][e0 & 3], qk_scale, -mb[qt]);
+        px[1] = __builtin_fmaf(s[2 * kk + (e1 >> 2)][qt][e1 & 3], qk_scale, -mb[qt]);
+        pin(px[0]);
+        pin(px[1]);
+      } else if constexpr (beat == 1) {
+        pe[0] = fast_exp2(px[0]);
+        pe[1] = fast_exp2(px[1]);
+        pin(pe[0]);
+        pin(pe[1]);
+      } else if constexpr (beat == 2) {
+        wd = pack2<T>(pe[0], pe[1]);
+        pin(wd);
+        pn[qt][kk][w] = wd;
+      } else {
+        big |= wd;
+        pin(big);
+      }
+    };
+
+    if constexpr (SM) {
+      if (EDGE) mask_block(s, k0);
+    }
+    if constexpr (SN) {
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const v8 a = as_vec8<T>(read_kmajor_operand<D>(vt, 32 * kk, dt * 16, g, c));
-        acc[dt][0] = mfma_16x16x32(a, as_vec8<T>(pf[0][kk]), acc[dt][0]);
-        acc[dt][1] = mfma_16x16x32(a, as_vec8<T>(pf[1][kk]), acc[dt][1]);
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) sn[kt][qt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    static_for<(LA < NM / QT ? LA : NM / QT)>([&](auto o) { read_op(o); });
+    if constexpr (SM && NM == 0) static_for<VS>([&](auto vv) { vslot(vv); });
+    if constexpr (NM < NC) static_for<NC>([&](auto cc) { copy_at(cc); });
+    static_for<NM>([&](auto ii) {
+      constexpr int i = decltype(ii)::value;
+      constexpr int o = i / QT, qt = i % QT;
+      if constexpr (qt == 0 && o + LA < NM / QT) read_op(std::integral_constant<int, o + LA>{});
+      if constexpr (NM >= NC && i % CSTRIDE == 1 && i / CSTRIDE < NC)
+        copy_at(std::integral_constant<int, i / CSTRIDE>{});
+      if constexpr (i < NA) {
+        constexpr int kk = o / (DT + 1), dt = (o % (DT + 1) + DT) % (DT + 1);
+        acc[dt][qt] = mfma_16x16x32(as_vec8<T>(opnd[o]), as_vec8<T>(pf[qt][kk]), acc[dt][qt]);
+      } else {
+        constexpr int b = o - NA / QT, kt = b / KS, ks = b % KS;
+        sn[kt][qt] = mfma_16x16x32(as_vec8<T>(opnd[o]), as_vec8<T>(qf[qt][ks]), sn[kt][qt]);
+      }
+      if constexpr (SM)
+        static_range<(i * VS + NM - 1) / NM, ((i + 1) * VS + NM - 1) / NM>([&](auto vv) { vslot(vv); });
+      TM_FENCE();
+    });
+    if constexpr (SM) {
+      /* some P reached 2: recompute this block's scores with K fragments read
+       * straight from HBM (its tile is being overwritten and its scores are no
+       * longer in registers), take the exact row maxima, move the offsets,
+       * redo P, and scale O and the row sums, which hold the P V of every
+       * block computed under the old offsets (all issued above) */
+      if (__builtin_amdgcn_ballot_w64((big & 0x40004000u) != 0) != 0) {
+        f32x4 sr[4][QT];
+        scores(sr, [&](int kt, int ks) {
+          const int key = min(k0 + kt * 16 + c, n - 1);
+          return *(const u32x4 *)(Kg + (int64_t)key * ss + ks * 32 + 8 * g);
+        });
+        mask_block(sr, k0);
+        float mx[QT];
+        row_max(sr, mx);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const float m_new = fmaxf(mb[qt], mx[qt] + BIAS);
+          const float alpha = fast_exp2(mb[qt] - m_new);
+          mb[qt] = m_new;
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const int e0 = 2 * w, e1 = 2 * w + 1;
+              const float p0 = fast_exp2(__builtin_fmaf(sr[2 * kk + (e0 >> 2)][qt][e0 & 3], qk_scale, -m_new));
+              const float p1 = fast_exp2(__builtin_fmaf(sr[2 * kk + (e1 >> 2)][qt][e1 & 3], qk_scale, -m_new));
+              pn[qt][kk][w] = pack2<T>(p0, p1);
+            }
+#pragma unroll
+          for (int dt = 0; dt <= DT; ++dt) acc[dt][qt] *= alpha;
+        }
       }
     }
     wait_vmem();
     __syncthreads();
   };
-  using Interior = std::integral_constant<bool, false>;
-  using Edge = std::integral_constant<bool, true>;
-
-  /* interior blocks (below every query of the workgroup, inside n) in pairs,
-   * then the masked rest */
-  const int n_interior = CAUSAL ? min(q0 / BN, n / BN) : n / BN;
-  int j = 0;
-  for (; j + 1 < n_interior; j += 2) {
-    step(Interior{}, lds_a, lds_b, j);
-    step(Interior{}, lds_b, lds_a, j + 1);
-  }
-  for (; j < nblocks; ++j) {
-    if ((j & 1) == 0) step(Edge{}, lds_a, lds_b, j);
-    else step(Edge{}, lds_b, lds_a, j);
-  }
-
-  /* epilogue: O = acc / l, L = m + log2(l) */
+  using T_ = std::integral_constant<bool, true>;
+  using F_ = std::integral_constant<bool, false>;
+  auto take_second_set = [&]() {
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) s[kt][qt] = s2[kt][qt];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      pf[qt][0] = pf2[qt][0];
+      pf[qt][1] = pf2[qt][1];
+    }
+  };
+
+  /* iteration j reads V(j-1) from vb[(j-1)&1] and K(j+1) from kb[(j+1)&1], and
+   * copies V(j) into vb[j&1] and K(j+2) into kb[j&1] */
+  iteration(F_{}, T_{}, T_{}, T_{}, vb1, kb1, vb0, kb0, 0, s, s2, pf, pf2);
+  take_second_set();
+  int j = 1;
+  /* interior pairs: blocks j-1 .. j+2 exist and j, j+1 need no mask */
+  for (; j + 2 < nblocks && j + 1 < first_edge; j += 2) {
+    iteration(T_{}, T_{}, T_{}, F_{}, vb0, kb0, vb1, kb1, j, s, s2, pf, pf2);
+    iteration(T_{}, T_{}, T_{}, F_{}, vb1, kb1, vb0, kb0, j + 1, s2, s, pf2, pf);
+  }
+  /* the rest, masked; j is odd here */
+  uint32_t vr = vb0, kr = kb0, vc = vb1, kc = kb1;
+  for (; j < nblocks; ++j) {
+    iteration(T_{}, T_{}, T_{}, T_{}, vr, kr, vc, kc, j, s, s2, pf, pf2);
+    take_second_set();
+    const uint32_t t0 = vr, t1 = kr;
+    vr = vc;
+    kr = kc;
+    vc = t0;
+    kc = t1;
+  }
+  iteration(T_{}, F_{}, F_{}, F_{}, vr, kr, vc, kc, j, s, s2, pf, pf2);
+
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
     const int qi = qw0 + qt * 16 + c;
-    const float l = group4_sum(l_i[qt]);
+    const float l = acc[DT][qt][0];
     if (qi < n) {
       const float inv = 1.f / l;
 #pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) {
+      for (int dt = 0; dt < DT; ++dt) {
         u32x2 w;
         w[0] = pack2<T>(acc[dt][qt][0] * inv, acc[dt][qt][1] * inv);
         w[1] = pack2<T>(acc[dt][qt][2] * inv, acc[dt][qt][3] * inv);
         *(u32x2 *)(Og + (int64_t)qi * ss + dt * 16 + 4 * g) = w;
       }
-      if (p.lse && g == 0) p.lse[(int64_t)bh * p.stride_lse + qi] = m_i[qt] + log2f(l);
+      if (p.lse && g == 0) p.lse[(int64_t)bh * p.stride_lse + qi] = mb[qt] + log2f(l);
     }
   }
 }

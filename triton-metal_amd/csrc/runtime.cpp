@@ -43,6 +43,15 @@
 #include "codeobject.h"
 #include "tm_args.h"
 
+/* Query rows and threads per workgroup of the specialised forward kernels
+ * (tm_attn_fwd_fast_*: 32 query rows per wave). */
+#ifndef TM_FWD_FAST_ROWS
+#define TM_FWD_FAST_ROWS 128
+#endif
+#ifndef TM_FWD_FAST_THREADS
+#define TM_FWD_FAST_THREADS 256
+#endif
+
 namespace {
 
 /* ---- errors ----------------------------------------------------------------
@@ -733,8 +742,8 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
       if (attn_fast_ok(spec, p.stride_head, p.stride_seq, p.n_ctx, p.sm_scale)) {
         plan.variant = format("tm_attn_fwd_fast_%s_d%d%s", el, spec.head_dim,
                               spec.causal ? "_causal" : "");
-        plan.grid[0] = (unsigned)(cdiv(p.n_ctx, 128) * heads);
-        plan.block = 256;
+        plan.grid[0] = (unsigned)(cdiv(p.n_ctx, TM_FWD_FAST_ROWS) * heads);
+        plan.block = TM_FWD_FAST_THREADS;
       } else {
         plan.variant = attn_symbol("fwd", spec);
         plan.grid[0] = (unsigned)cdiv(p.n_ctx, 64);
