@@ -317,18 +317,25 @@ def cpu_baseline(target_seconds):
             break
     flops = attention_flops(heads, seq, dim, True) + attention_flops(heads, seq, dim, True,
                                                                      backward=True)
-    threads = os.cpu_count()
+    host_cpus = os.cpu_count()
+    blas_threads, blas_library = None, None
     try:
         from threadpoolctl import threadpool_info
         info = [x for x in threadpool_info() if x.get("user_api") == "blas"]
         if info:
-            threads = int(info[0]["num_threads"])
+            blas_threads = int(info[0]["num_threads"])
+            blas_library = info[0].get("internal_api")
     except Exception:
         pass
     return {
         "value": round(flops / elapsed / 1e12, 6),
         "unit": "TFLOP/s",
-        "cores": threads,
+        # the threads the BLAS calls ran on (the whole of the work); the host's
+        # logical CPUs beside it
+        "cores": blas_threads if blas_threads else host_cpus,
+        "host_cpus": host_cpus,
+        "blas_threads": blas_threads,
+        "blas_library": blas_library,
         "kind": "port",
         "sample": (f"{heads} (batch,head) slices of config 5 (S4096 D128 causal) forward+backward "
                    f"in numpy fp32 BLAS, {elapsed:.1f} s"),
@@ -361,8 +368,8 @@ def main():
     if not core.is_usable():
         raise SystemExit("no usable gfx950 device: " + str(core.unusable_reason()))
     if args.probes:
-        from triton_metal import probes
-        print(json.dumps({"probes": probes.run(), "device": core.device_name()}))
+        import bench_probes
+        print(json.dumps({"probes": bench_probes.run(), "device": core.device_name()}))
         return
     if args.profile_pass:
         profile_pass(core, ops)

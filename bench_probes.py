@@ -20,7 +20,7 @@ Run: python bench.py --probes
 
 import json
 
-from . import _core
+from triton_metal import _core
 
 CUS = 256
 CLOCK_HZ = 2.4e9

@@ -24,8 +24,12 @@
  *         attn_bwd_dkdv, sae_encode_kernel (relu(x @ W + b),
  *         Sources/TritonMetalMLX/SAEEncoder.swift:29-40), tm_probe.
  *   - a "buffer" is device memory in HBM (hipMalloc).  tm_buffer_contents
- *     returns its device address (what a kernel sees); host access goes
- *     through tm_buffer_write / tm_buffer_read.
+ *     gives it a host-addressable mirror (pinned host memory) that stands in
+ *     for the reference's unified memory: while the mirror exists, host
+ *     writes through it reach the kernels of later launches and the results
+ *     of a launch are in it when the launch returns (a launch that binds such
+ *     a buffer copies it to HBM before the dispatch and back afterwards, and
+ *     waits).  Buffers never mapped this way are not copied.
  *   - launches run on one library-owned HIP stream.
  */
 #ifndef TRITONMETAL_H
@@ -94,13 +98,15 @@ int32_t tm_release_kernel(int64_t kernel);
 
 /* length > 0 bytes of HBM -> buffer handle, 0 on failure.  Replaces Compiler.swift:296. */
 int64_t tm_alloc_buffer(int64_t length);
-/* Device address of the buffer, NULL on failure.  Replaces Compiler.swift:307. */
+/* Host address of the buffer's contents (its host mirror, created and filled
+ * from HBM on the first call), NULL on failure.  Replaces Compiler.swift:307. */
 void *tm_buffer_contents(int64_t buffer);
 /* Replaces Compiler.swift:317 tm_buffer_length. */
 int64_t tm_buffer_length(int64_t buffer);
 /* Host -> device copy, bounds-checked; 0 / -1.  Replaces Compiler.swift:328. */
 int32_t tm_buffer_write(int64_t buffer, int64_t offset, const void *source, int64_t length);
-/* Device -> host copy, bounds-checked; 0 / -1.  Replaces Compiler.swift:338. */
+/* Device -> host copy (from the mirror when the buffer has one), bounds-checked;
+ * 0 / -1.  Replaces Compiler.swift:338. */
 int32_t tm_buffer_read(int64_t buffer, int64_t offset, void *destination, int64_t length);
 /* Replaces Compiler.swift:373 tm_free_buffer. */
 int32_t tm_free_buffer(int64_t buffer);

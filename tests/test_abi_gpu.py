@@ -123,16 +123,95 @@ def test_compile_errors_surface_as_zero_handle(core, device):
     assert "HIP compilation failed" in core.last_error()
 
 
-def test_buffer_contents_is_the_device_address(core, device):
-    handle = core.alloc_buffer(16)
+def _host_view(core, handle, n):
+    """What the reference's MetalBuffer._view() builds (python/triton_metal/
+    buffer.py:62-63): a ctypes array over tm_buffer_contents."""
+    return (ctypes.c_float * n).from_address(core.buffer_contents(handle))
+
+
+def test_buffer_contents_is_a_host_view(core, device):
+    """tm_buffer_contents is host-addressable, as the reference's unified
+    memory is: values written with tm_buffer_write are visible through it,
+    values written through it reach tm_buffer_read and the next launch, and a
+    launch's results are in it when the launch returns."""
+    src = _upload(core, [float(i) for i in range(64)])
+    dst = core.alloc_buffer(256)
+    library = core.compile_msl(COPY)
+    kernel = core.load_kernel(library, "copy_kernel")
     try:
-        assert core.buffer_contents(handle) % 256 == 0
-        value = ctypes.c_float(1.25)
-        core.buffer_write(handle, 4, ctypes.addressof(value), 4)
-        out = _download(core, handle, 2)
-        assert out[1] == 1.25
+        view = _host_view(core, src, 64)
+        assert core.buffer_contents(src) % 16 == 0
+        assert list(view) == [float(i) for i in range(64)]
+        for i in range(64):
+            view[i] = 100.0 + i                  # host writes through the pointer
+        assert list(_download(core, src, 64)) == [100.0 + i for i in range(64)]
+        out = _host_view(core, dst, 64)          # mapped before the launch
+        core.launch(kernel, (1, 1, 1), 64, [core.ARG_BUFFER] * 2, [src, dst])
+        assert list(out) == [100.0 + i for i in range(64)]
+        assert list(_download(core, dst, 64)) == [100.0 + i for i in range(64)]
+        value = ctypes.c_float(-2.5)
+        core.buffer_write(src, 8, ctypes.addressof(value), 4)
+        assert view[2] == -2.5
+        # the reference's tolist(): list(self._view())
+        assert list(_host_view(core, src, 4)) == [100.0, 101.0, -2.5, 103.0]
+    finally:
+        core.free_buffer(src)
+        core.free_buffer(dst)
+        core.release_kernel(kernel)
+        core.release_library(library)
+
+
+def test_host_view_of_a_kernel_output_mapped_after_the_launch(core, device):
+    src = _upload(core, [float(i) for i in range(64)])
+    dst = core.alloc_buffer(256)
+    library = core.compile_msl(COPY)
+    kernel = core.load_kernel(library, "copy_kernel")
+    try:
+        core.launch(kernel, (1, 1, 1), 64, [core.ARG_BUFFER] * 2, [src, dst])
+        assert list(_host_view(core, dst, 64)) == [float(i) for i in range(64)]
+    finally:
+        core.free_buffer(src)
+        core.free_buffer(dst)
+        core.release_kernel(kernel)
+        core.release_library(library)
+
+
+def test_copy_bounds_do_not_wrap(core, device):
+    handle = core.alloc_buffer(16)
+    byte = ctypes.c_uint8(0)
+    try:
+        assert core._lib.tm_buffer_write(handle, 2**63 - 1, ctypes.addressof(byte), 1) == -1
+        assert "exceeds the" in core.last_error()
+        assert core._lib.tm_buffer_read(handle, 15, ctypes.addressof(byte), 2**63 - 1) == -1
+        assert "exceeds the" in core.last_error()
+        assert core._lib.tm_buffer_read(handle, 15, ctypes.addressof(byte), 1) == 0
     finally:
         core.free_buffer(handle)
+
+
+def test_async_launch_survives_releasing_its_handles(core, device):
+    """A dispatch still queued when its kernel and library are released runs to
+    completion: the library drains its stream before unloading the code object."""
+    n = 1 << 20
+    a = _upload(core, [1.0] * n)
+    b = _upload(core, [2.0] * n)
+    out = core.alloc_buffer(4 * n)
+    library = core.compile_msl(VECTOR_ADD)
+    kernel = core.load_kernel(library, "add_kernel")
+    try:
+        B, I = core.ARG_BUFFER, core.ARG_I32
+        for _ in range(4):
+            assert core._lib.tm_launch_async(kernel, n // 1024, 1, 1, 256,
+                                             (ctypes.c_int32 * 4)(B, B, B, I),
+                                             (ctypes.c_int64 * 4)(a, b, out, n), 4) == 0
+        core.release_kernel(kernel)
+        core.release_library(library)
+        assert core._lib.tm_synchronize() == 0
+        got = _download(core, out, n)
+        assert got[0] == 3.0 and got[n - 1] == 3.0
+    finally:
+        for h in (a, b, out):
+            core.free_buffer(h)
 
 
 def test_code_object_loading_through_the_abi(core, device, tmp_path):
@@ -337,3 +416,33 @@ def test_user_launches_must_bind_the_declared_arguments(core, device, tmp_path):
         core.free_buffer(out)
         core.release_kernel(kernel)
         core.release_library(library)
+
+
+@pytest.mark.parametrize("element", ["bf16", "f32"])
+def test_batch_in_z_grid_matches_flattened_heads(core, device, element):
+    """The reference's callers put B*H in program_id(1) (attention_training.py:
+    223-246); a caller that carries the batch in z, grid (cdiv(S, BLOCK_M), H, B),
+    gets the same results as the flattened (cdiv(S, BLOCK_M), B*H, 1): the
+    built-ins take heads = gy * gz."""
+    from triton_metal import ops
+    batch, heads, seq, dim = 2, 3, 96, 64
+    rng = np.random.default_rng(5)
+    layer = ops.AttentionLayer(batch * heads, seq, dim, element, causal=True)
+    try:
+        for name in ("q", "k", "v", "do"):
+            layer.upload(name, rng.standard_normal((batch * heads, seq, dim), dtype=np.float32))
+        kern = layer.lib.kernels
+        results = []
+        for split in (False, True):
+            for name, (grid, kinds, values) in (("attn_fwd", layer.fwd_args()),
+                                                ("attn_bwd_preprocess", layer.pre_args()),
+                                                ("attn_bwd_dq", layer.dq_args()),
+                                                ("attn_bwd_dkdv", layer.dkdv_args())):
+                if split:
+                    grid = (grid[0], heads, batch)
+                core.launch(kern[name], grid, 128, kinds, values)
+            results.append({n: layer.read(n) for n in ("o", "lse", "dq", "dk", "dv")})
+        for n in results[0]:
+            assert np.array_equal(results[0][n], results[1][n]), n
+    finally:
+        layer.free()

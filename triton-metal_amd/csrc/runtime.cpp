@@ -229,7 +229,12 @@ struct Library : Object {
    * (empty when the image carries none this library can read) */
   std::map<std::string, std::vector<tm_codeobject::ArgSlot>> signatures;
   ~Library() override {
-    if (module) (void)hipModuleUnload(module);
+    if (!module) return;
+    /* a dispatch of one of its kernels may still be queued (tm_launch_async):
+     * drain the library stream before the code object goes away */
+    Device &dev = device();
+    if (dev.present) (void)hipStreamSynchronize(dev.stream);
+    (void)hipModuleUnload(module);
   }
 };
 
@@ -247,11 +252,23 @@ struct Kernel : Object {
   std::string last_variant;
 };
 
+/* A buffer lives in HBM.  tm_buffer_contents gives it a host mirror (pinned
+ * host memory, filled from HBM on that first call): the host address a
+ * reference caller reads and writes through, as it does the unified memory
+ * of the reference's buffers (Compiler.swift:306-311).  While a mirror exists
+ * it is the buffer's contents outside launches: tm_buffer_write updates both
+ * copies, tm_buffer_read reads the mirror, and a launch that binds the buffer
+ * copies the mirror to HBM before the dispatch and back after it completes
+ * (the launch then waits, even tm_launch_async).  Buffers without a mirror
+ * (the hot path) are never copied. */
 struct Buffer : Object {
   Kind kind() const override { return Kind::Buffer; }
   void *ptr = nullptr;
   int64_t length = 0;
+  void *host = nullptr; /* the mirror, once tm_buffer_contents was called */
+  std::mutex host_lock;
   ~Buffer() override {
+    if (host) (void)hipHostFree(host);
     if (ptr) (void)hipFree(ptr);
   }
 };
@@ -1025,10 +1042,19 @@ void enqueue(const Plan &plan, hipStream_t stream) {
  * except the device lookup the built-in planner needs. */
 Plan prepare(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads,
              const int32_t *kinds, const int64_t *values, int32_t argc,
-             std::shared_ptr<Kernel> &k_out) {
+             std::shared_ptr<Kernel> &k_out,
+             std::vector<std::shared_ptr<Buffer>> *mirrored = nullptr) {
   auto k = handles().lookup<Kernel>(kernel, Kind::Kernel, "kernel");
   k_out = k;
   std::vector<Arg> args = decode_args(kinds, values, argc);
+  if (mirrored)
+    for (const Arg &a : args)
+      if (a.buffer) {
+        std::lock_guard<std::mutex> guard(a.buffer->host_lock);
+        if (a.buffer->host &&
+            std::find(mirrored->begin(), mirrored->end(), a.buffer) == mirrored->end())
+          mirrored->push_back(a.buffer);
+      }
   if (gx <= 0 || gy <= 0 || gz <= 0)
     throw TmError("threadgroup grid must be positive in every dimension");
   if (gx > 0x7fffffff || gy > 0xffff || gz > 0xffff)
@@ -1129,11 +1155,28 @@ int64_t launch_common(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_
                       const int32_t *kinds, const int64_t *values, int32_t argc, bool wait,
                       int32_t repeats, float *elapsed_ms) {
   std::shared_ptr<Kernel> k;
-  Plan plan = prepare(kernel, gx, gy, gz, threads, kinds, values, argc, k);
+  std::vector<std::shared_ptr<Buffer>> mirrored;
+  Plan plan = prepare(kernel, gx, gy, gz, threads, kinds, values, argc, k, &mirrored);
   Device &dev = require_device();
+  /* buffers with a host mirror: mirror -> HBM before, HBM -> mirror after */
+  for (const auto &b : mirrored) {
+    std::lock_guard<std::mutex> guard(b->host_lock);
+    hip_check(hipMemcpyAsync(b->ptr, b->host, (size_t)b->length, hipMemcpyHostToDevice, dev.stream),
+              "hipMemcpyAsync (host mirror to HBM)");
+  }
+  auto refresh_mirrors = [&]() {
+    if (mirrored.empty()) return;
+    finish(dev.stream);
+    for (const auto &b : mirrored) {
+      std::lock_guard<std::mutex> guard(b->host_lock);
+      hip_check(hipMemcpy(b->host, b->ptr, (size_t)b->length, hipMemcpyDeviceToHost),
+                "hipMemcpy (HBM to host mirror)");
+    }
+  };
   if (repeats <= 0) {
     enqueue(plan, dev.stream);
     if (wait) finish(dev.stream);
+    refresh_mirrors();
     return 0;
   }
   hipEvent_t start, stop;
@@ -1150,6 +1193,7 @@ int64_t launch_common(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_
   float ms = 0.f;
   hip_check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
   if (elapsed_ms) *elapsed_ms = ms;
+  refresh_mirrors();
   return 0;
 }
 
@@ -1360,7 +1404,26 @@ int64_t tm_alloc_buffer(int64_t length) {
 
 void *tm_buffer_contents(int64_t buffer) {
   TM_GUARD_BEGIN
-  return handles().lookup<Buffer>(buffer, Kind::Buffer, "buffer")->ptr;
+  auto buf = handles().lookup<Buffer>(buffer, Kind::Buffer, "buffer");
+  std::lock_guard<std::mutex> guard(buf->host_lock);
+  if (!buf->host) {
+    Device &dev = require_device();
+    finish(dev.stream);
+    void *host = nullptr;
+    hipError_t status = hipHostMalloc(&host, (size_t)buf->length, hipHostMallocDefault);
+    if (status != hipSuccess) {
+      (void)hipGetLastError();
+      throw TmError(format("could not allocate the %lld-byte host mirror of buffer %lld (%s)",
+                           (long long)buf->length, (long long)buffer, hipGetErrorName(status)));
+    }
+    status = hipMemcpy(host, buf->ptr, (size_t)buf->length, hipMemcpyDeviceToHost);
+    if (status != hipSuccess) {
+      (void)hipHostFree(host);
+      hip_check(status, "hipMemcpy (HBM to host mirror)");
+    }
+    buf->host = host;
+  }
+  return buf->host;
   TM_GUARD_END(nullptr)
 }
 
@@ -1376,7 +1439,8 @@ static int32_t tm_copy(int64_t buffer, int64_t offset, const void *host, int64_t
   if (!host || length < 0 || offset < 0)
     throw TmError("buffer copy received invalid bounds");
   auto buf = handles().lookup<Buffer>(buffer, Kind::Buffer, "buffer");
-  if (offset + length > buf->length)
+  /* written so that no sum can wrap */
+  if (length > buf->length || offset > buf->length - length)
     throw TmError(format("copy of %lld bytes at offset %lld exceeds the %lld-byte buffer",
                          (long long)length, (long long)offset, (long long)buf->length));
   if (length == 0) return 0;
@@ -1384,10 +1448,16 @@ static int32_t tm_copy(int64_t buffer, int64_t offset, const void *host, int64_t
   /* Work queued on the library stream is ordered before the copy. */
   finish(dev.stream);
   char *dptr = (char *)buf->ptr + offset;
-  if (to_device)
+  std::lock_guard<std::mutex> guard(buf->host_lock);
+  char *mirror = buf->host ? (char *)buf->host + offset : nullptr;
+  if (to_device) {
     hip_check(hipMemcpy(dptr, host, (size_t)length, hipMemcpyHostToDevice), "hipMemcpy");
-  else
+    if (mirror) memcpy(mirror, host, (size_t)length);
+  } else if (mirror) {
+    memcpy((void *)host, mirror, (size_t)length);
+  } else {
     hip_check(hipMemcpy((void *)host, dptr, (size_t)length, hipMemcpyDeviceToHost), "hipMemcpy");
+  }
   return 0;
   TM_GUARD_END(-1)
 }

@@ -1,10 +1,14 @@
 """A `.data_ptr()` object over a library-owned HBM buffer.
 
 Counterpart of the reference's MetalBuffer (python/triton_metal/buffer.py:35-114):
-same constructor, dtype names, `data_ptr`, `copy_from`/`copy_to`, `numpy`,
-`from_numpy`, `tolist`, `free`.  On MI355X the buffer lives in device memory,
-so `data_ptr()` is the device address a kernel sees and every host access is
-a `tm_buffer_read`/`tm_buffer_write` copy; there is no host-mapped view.
+same constructor arguments, dtype names, `data_ptr`, `copy_from`/`copy_to`,
+`numpy`, `from_numpy`, `tolist`, `free`.  On MI355X the buffer lives in device
+memory.  `data_ptr()` is `tm_buffer_contents`: a host address that behaves like
+the reference's unified memory (the library keeps a pinned host mirror of a
+buffer once it has been asked for one, and copies it around each launch that
+binds the buffer), so code that reads or writes through it works unchanged.
+The copies `copy_from`/`copy_to`/`numpy`/`write` are `tm_buffer_write`/
+`tm_buffer_read` and never create a mirror.
 
 numpy has no bfloat16: bf16 buffers exchange raw 16-bit words (np.uint16), and
 `bf16_bits` / `bf16_values` convert (round-to-nearest-even).
@@ -52,25 +56,28 @@ def round_to(values, dtype: str) -> np.ndarray:
     return x.copy()
 
 
+def _element_name(dtype) -> str:
+    """'float32', np.float32, torch.bfloat16, 'bfloat16' ... -> the bare element
+    name the size table uses."""
+    name = str(dtype).rsplit(".", 1)[-1]
+    if name not in _ITEMSIZE:
+        raise TypeError(f"unsupported dtype {dtype!r}; expected one of {sorted(_ITEMSIZE)}")
+    return name
+
+
 class DeviceBuffer:
     """HBM the GPU reads and writes; the host moves bytes in and out."""
 
     def __init__(self, shape, dtype="float32"):
-        if isinstance(shape, int):
-            shape = (shape, )
-        dtype = str(dtype).split(".")[-1]
-        if dtype not in _ITEMSIZE:
-            raise TypeError(f"unsupported dtype {dtype!r}; expected one of {sorted(_ITEMSIZE)}")
-        self.shape = tuple(shape)
-        self.dtype = dtype
-        self.numel = 1
-        for d in self.shape:
-            self.numel *= d
-        self.itemsize = _ITEMSIZE[dtype]
+        self.shape = (shape,) if isinstance(shape, int) else tuple(int(d) for d in shape)
+        self.dtype = _element_name(dtype)
+        self.itemsize = _ITEMSIZE[self.dtype]
+        self.numel = int(np.prod(self.shape, dtype=np.int64))
         self.nbytes = self.numel * self.itemsize
         self.tm_handle = _core.alloc_buffer(self.nbytes)
 
     def data_ptr(self):
+        """Host address of the contents (the buffer's host mirror)."""
         return _core.buffer_contents(self.tm_handle)
 
     def __len__(self):

@@ -201,25 +201,31 @@ class AttentionLayer:
     stride_head = S*D and stride_seq = D (AttentionKernel.swift:25-28).
     """
 
+    #: per-(head, row) tensors: the forward's L (log2 units) and the backward's Delta
+    ROW_STATS = ("lse", "delta")
+    #: per-(head, row, d) tensors in the element type
+    TENSORS = ("q", "k", "v", "o", "do", "dq", "dk", "dv")
+
     def __init__(self, heads, seq, dim, element="f32", causal=False, scale=None,
                  block_m=16, block_n=32):
         self.heads, self.seq, self.dim = heads, seq, dim
-        self.element = element
-        self.causal = causal
+        self.element, self.causal = element, causal
+        # the reference caller's tile sizes only shape the requested grids; the
+        # library covers the problem with its own tiles
         self.block_m, self.block_n = block_m, block_n
-        self.scale = 1.0 / math.sqrt(dim) if scale is None else scale
+        self.scale = scale if scale is not None else 1.0 / math.sqrt(dim)
         self.lib = library(element, dim, causal)
-        dtype = _ELEMENTS[element]
-        shape = (heads, seq, dim)
-        self.buffers = {name: DeviceBuffer(shape, dtype) for name in
-                        ("q", "k", "v", "o", "do", "dq", "dk", "dv")}
-        self.buffers["lse"] = DeviceBuffer((heads, seq), "float32")
-        self.buffers["delta"] = DeviceBuffer((heads, seq), "float32")
+        self.buffers = {}
+        for name in self.TENSORS:
+            self.buffers[name] = DeviceBuffer((heads, seq, dim), _ELEMENTS[element])
+        for name in self.ROW_STATS:
+            self.buffers[name] = DeviceBuffer((heads, seq), "float32")
 
     def free(self):
-        for buffer in self.buffers.values():
+        """Release every buffer (the library stays cached for other layers)."""
+        while self.buffers:
+            _, buffer = self.buffers.popitem()
             buffer.free()
-        self.buffers = {}
 
     def upload(self, name, array):
         self.buffers[name].write(np.asarray(array, dtype=np.float32)
