@@ -16,9 +16,8 @@
  *   - O^T = V^T P^T keeps the lane <-> query ownership, so P goes from the
  *     softmax straight into the B operand; a ones tile beside V^T gives l;
  *   - K and V tiles [64 keys][D] are double-buffered in LDS in their natural
- *     row order, 16-byte chunks XOR-swizzled by row, each tile with the key
- *     that suits its reads; K feeds the A operand by ds_read_b128, V^T by the
- *     transposing ds_read_b64_tr_b16;
+ *     row order, 16-byte chunks XOR-swizzled by row (KEY_BOTH); K feeds the
+ *     A operand by ds_read_b128, V^T by the transposing ds_read_b64_tr_b16;
  *   - causal: key blocks past the workgroup's last query are never visited,
  *     masking only runs on blocks that straddle the diagonal or n_ctx (a wave
  *     whose queries all lie below a block computes it fully masked: skipping
@@ -89,31 +88,36 @@ TM_DEV void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 /* 16-byte chunk position of logical chunk `chunk` in row `row`: the chunk
  * XORed with a key of the row.  Two read patterns meet the tiles: 16
- * consecutive rows at one chunk (ds_read_b128) and 8 consecutive rows at a
- * chunk pair (ds_read_b64_tr_b16).  No key serves both without conflicts.
- * KEY_TR keeps the transposed reads conflict-free (D = 128: rows are 256
- * bytes, the key spreads 16 rows over the 16 chunk positions with even keys
- * for rows 0-7 of each group of 16; D = 64: rows are 128 bytes, row parity
- * picks the half, the key spreads each parity class the same way); tiles read
- * both ways keep it, as keys with fewer b128 conflicts measured slower there.
- * KEY_B128 serves tiles read only by ds_read_b128. */
+ * consecutive rows at one chunk (ds_read_b128 of an MFMA operand) and 8
+ * consecutive rows at a chunk pair (ds_read_b64_tr_b16 of a k-major operand).
+ * KEY_BOTH serves both at full LDS rate; it was found by timing every
+ * GF(2)-linear key of the row's low four bits (3 bits at D = 64) on both
+ * patterns at once (8 waves per CU, 16 reads in flight per wave): at D = 128
+ * it reads within 1% of the best key for each pattern (the row-index key
+ * loses 5% on 16-row reads and 30% on transposed reads, the rotate key of the
+ * transposed reads 50% on 16-row reads); at D = 64 within 1%.
+ * KEY_B128 (the row index) and KEY_TR (a rotation of it) are the
+ * per-pattern keys, kept for comparison. */
 enum SwizzleKey {
-  KEY_TR = 0,   /* tiles read both ways, or by the transposing reads only */
-  KEY_B128 = 1  /* tiles read only by ds_read_b128 of 16 consecutive rows */
+  KEY_TR = 0,   /* transposed reads only */
+  KEY_B128 = 1, /* ds_read_b128 of 16 consecutive rows only */
+  KEY_BOTH = 2  /* both */
 };
 
-template <int D, int KEY = KEY_TR>
+template <int D, int KEY = KEY_BOTH>
 TM_DEV int swz(int row) {
-  /* row & 15 (D = 128) and row & 7 (D = 64) leave the 16-row ds_read_b128
-   * pattern with no bank conflicts (SQ_LDS_BANK_CONFLICT reads 0; the shared
-   * key conflicts on a third of the forward's LDS cycles) */
+  if (KEY == KEY_BOTH) {
+    /* linear over GF(2) in row bits 0..3: the key of each bit */
+    if (D == 128) return ((row & 1) ? 5 : 0) ^ ((row & 2) ? 9 : 0) ^ ((row & 4) ? 10 : 0) ^ ((row & 8) ? 7 : 0);
+    return ((row & 1) ? 7 : 0) ^ ((row & 2) ? 4 : 0) ^ ((row & 4) ? 4 : 0) ^ ((row & 8) ? 6 : 0);
+  }
   if (KEY == KEY_B128) return D == 128 ? (row & 15) : (row & 7);
   if (D == 128) return ((row & 7) << 1) | ((row >> 3) & 1);
   const int t = row >> 1;
   return ((t & 3) << 1) | ((t >> 2) & 1);
 }
 
-template <int D, int KEY = KEY_TR>
+template <int D, int KEY = KEY_BOTH>
 TM_DEV int tile_off(int row, int chunk) {
   return row * (D * 2) + ((chunk ^ swz<D, KEY>(row)) << 4);
 }
@@ -125,7 +129,7 @@ TM_DEV int tile_off(int row, int chunk) {
  * resource, so the hardware delivers zeros for them (finite values that the
  * caller masks: scores to -inf, P to 0).  The host only takes this path when a
  * head's rows span fewer than 2^31 bytes. */
-template <typename T, int D, int ROWS, int KEY = KEY_TR>
+template <typename T, int D, int ROWS, int KEY = KEY_BOTH>
 TM_DEV void stage_rows(const T *src, int64_t ss, int k0, int n, char *tile, int wave, int lane) {
   constexpr int CPR = D / 8;                      /* 16-byte chunks per row */
   constexpr int RPI = 64 / CPR;                   /* rows per wave instruction */
@@ -183,8 +187,8 @@ TM_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
  * row maxima.
  *
  * LDS: K and V tiles double-buffered, in their natural row order with the
- * 16-byte chunks XOR-swizzled (KEY_B128 for K, read by ds_read_b128; KEY_TR
- * for V, read transposed).  Iteration j reads V(j-1) and K(j+1) and copies
+ * 16-byte chunks XOR-swizzled with KEY_BOTH (K is read by ds_read_b128, V
+ * transposed).  Iteration j reads V(j-1) and K(j+1) and copies
  * V(j) and K(j+2) into the buffers that V(j-2) and K(j) left; the copy
  * instructions are spread over the MFMA stream (issued back to back they stall
  * the wave on the memory pipeline for hundreds of cycles).
@@ -314,8 +318,8 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   /* blocks [0, first_edge) need no mask */
   const int first_edge = CAUSAL ? min(q0 / BN, n / BN) : n / BN;
 
-  TileCopy<T, D, BN, KEY_B128> kcp;
-  TileCopy<T, D, BN, KEY_TR> vcp;
+  TileCopy<T, D, BN, KEY_BOTH> kcp;
+  TileCopy<T, D, BN, KEY_BOTH> vcp;
   kcp.init(ss, wave, lane);
   vcp.init(ss, wave, lane);
   if (nblocks > 0) kcp.copy(Kg, ss, 0, n, kb0, wave);
@@ -333,7 +337,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
    * transposed read are immediates */
   uint32_t koff[KS], voff[DT];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) koff[ks] = (uint32_t)tile_off<D, KEY_B128>(c, ks * 4 + g);
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = (uint32_t)tile_off<D>(c, ks * 4 + g);
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
     voff[dt] = (uint32_t)(tile_off<D>(4 * g + (c >> 2), 2 * dt + ((c & 3) >> 1)) + ((c & 1) << 3));
