@@ -79,7 +79,8 @@ COPY_BYTES = 1 << 30
 def profile_pass(core, ops):
     """One copy of COPY_BYTES (reads and writes that many bytes of HBM), then one
     dispatch each of attn_fwd, attn_bwd_preprocess, attn_bwd_dq, attn_bwd_dkdv at
-    config 5, matmul_kernel at config 3 and sae_encode_kernel at 8192 x 2048 x 16384."""
+    config 5, the bwd=atomic backward (attn_bwd_fused: accumulator clear, fused
+    kernel, dQ conversion) at config 5, matmul_kernel at config 3 and sae_encode_kernel at 8192 x 2048 x 16384."""
     from triton_metal.buffer import DeviceBuffer
     lib = core.compile_msl(COPY_SOURCE)
     kernel = core.load_kernel(lib, "tm_calibration_copy")
@@ -96,6 +97,12 @@ def profile_pass(core, ops):
     layer.run_forward()
     layer.run_backward()
     layer.free()
+    fused = ops.AttentionLayer(B * H, S, D, "bf16", True, bwd="atomic")
+    for i, name in enumerate(("q", "k", "v", "do")):
+        fused.buffers[name].write(normal_bf16((B * H, S, D), 100 + i))
+    fused.run_forward()
+    fused.run_backward()
+    fused.free()
     n = 8192
     a = DeviceBuffer((n, n), "bfloat16").write(normal_bf16((n, n), 1))
     b = DeviceBuffer((n, n), "bfloat16").write(normal_bf16((n, n), 2))
@@ -134,9 +141,9 @@ def kernel_ms(core, kernel, grid, kinds, values, sample_ms):
 
 
 def bench_attention(core, ops, batch, heads, seq, dim, causal, steps, warmup, sample_ms,
-                    backward=True, element="bf16"):
+                    backward=True, element="bf16", bwd="split"):
     bh = batch * heads
-    layer = ops.AttentionLayer(bh, seq, dim, element, causal)
+    layer = ops.AttentionLayer(bh, seq, dim, element, causal, bwd=bwd)
     try:
         for i, name in enumerate(("q", "k", "v", "do")):
             x = normal_bf16((bh, seq, dim), 100 + i)
@@ -146,7 +153,10 @@ def bench_attention(core, ops, batch, heads, seq, dim, causal, steps, warmup, sa
             layer.buffers[name].write(x)
         kern = layer.lib.kernels
         launches = [("attn_fwd", layer.fwd_args(True))]
-        if backward:
+        if backward and bwd == "atomic":
+            launches += [("attn_bwd_preprocess", layer.pre_args()),
+                         ("attn_bwd_fused", layer.fused_args())]
+        elif backward:
             launches += [("attn_bwd_preprocess", layer.pre_args()),
                          ("attn_bwd_dq", layer.dq_args()),
                          ("attn_bwd_dkdv", layer.dkdv_args())]
@@ -424,6 +434,15 @@ def main():
         components["fa2_fwd_config4"] = {"tflops": round(f4 / (ms4 * 1e-3) / 1e12, 2),
                                          "frac_of_peak": round(f4 / (ms4 * 1e-3) / 1e12 / 2500, 4),
                                          "ms": round(ms4, 4), "variant": k4["attn_fwd"]["variant"]}
+        # the opt-in single-pass backward (bwd=atomic) at config 5, beside the split one
+        _, ka = bench_attention(core, ops, B, H, S, D, True, 0, args.warmup, args.sample_ms,
+                                bwd="atomic")
+        ms_a = ka["attn_bwd_preprocess"]["ms"] + ka["attn_bwd_fused"]["ms"]
+        components["fa2_bwd_atomic"] = {
+            "tflops": round(f_bwd / (ms_a * 1e-3) / 1e12, 2),
+            "frac_of_peak": round(f_bwd / (ms_a * 1e-3) / 1e12 / 2500, 4),
+            "ms": round(ms_a, 4), "fused_ms": round(ka["attn_bwd_fused"]["ms"], 4),
+            "vs_split": round(bwd_ms / ms_a, 3), "variant": ka["attn_bwd_fused"]["variant"]}
         # fp16 variant of config 5 (the reference's own attention element type)
         _, k16 = bench_attention(core, ops, B, H, S, D, True, 0, args.warmup, args.sample_ms,
                                  element="f16")

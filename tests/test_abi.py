@@ -120,6 +120,10 @@ def test_builtin_spec_round_trips_through_emit(core):
     assert core.emit_msl("builtin element=bf16 head_dim=128 causal=1") == \
         "builtin element=bf16 head_dim=128 causal=1"
     assert core.emit_msl("builtin") == "builtin element=f32 head_dim=64 causal=0"
+    assert core.emit_msl("builtin element=bf16 bwd=split") == \
+        "builtin element=bf16 head_dim=64 causal=0"
+    assert core.emit_msl("builtin element=bf16 head_dim=128 bwd=atomic") == \
+        "builtin element=bf16 head_dim=128 causal=0 bwd=atomic"
 
 
 @pytest.mark.parametrize("spec,message", [
@@ -127,6 +131,7 @@ def test_builtin_spec_round_trips_through_emit(core):
     ("builtin head_dim=0", "head_dim must be an integer in 1..128"),
     ("builtin head_dim=129", "head_dim must be an integer in 1..128"),
     ("builtin causal=2", "causal must be 0 or 1"),
+    ("builtin bwd=fast", "bwd must be split or atomic"),
     ("builtin colour=red", "unknown key 'colour'"),
     ("builtin element", "expected key=value"),
 ])
@@ -153,6 +158,23 @@ def test_kernel_info_publishes_every_builtin(core):
     assert len(dkdv["args"]) == 13
     for k in kernels.values():
         assert k["threads_per_threadgroup"] > 0 and k["block_size"] > 0
+
+
+def test_fused_backward_is_offered_only_with_bwd_atomic(core):
+    split = json.loads(core.kernel_info("builtin element=bf16 head_dim=128 causal=1"))
+    assert "attn_bwd_fused" not in {k["name"] for k in split["kernels"]}
+    info = json.loads(core.kernel_info("builtin element=bf16 head_dim=128 causal=1 bwd=atomic"))
+    fused = {k["name"]: k for k in info["kernels"]}["attn_bwd_fused"]
+    # Q, K, V, dO, dQ, dK, dV, L, Delta, sm_scale, stride_head, stride_seq,
+    # stride_lse, n_ctx: the dK/dV list with dQ inserted before dK
+    assert [a["kind"] for a in fused["args"]] == [0] * 9 + [2, 1, 1, 1, 1]
+    assert [a["dtype"] for a in fused["args"]] == ["bf16"] * 7 + ["f32"] * 3 + ["i32"] * 4
+    lib = core.compile_msl("builtin element=bf16 head_dim=128 causal=1")
+    try:
+        with pytest.raises(RuntimeError, match="bwd=atomic"):
+            core.load_kernel(lib, "attn_bwd_fused")
+    finally:
+        core.release_library(lib)
 
 
 def test_sae_encoder_declares_the_arguments_its_wrapper_binds(core):

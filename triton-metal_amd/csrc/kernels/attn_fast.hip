@@ -826,8 +826,8 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
  * are independent, so the wave's VALU work overlaps its MFMA work.  Buffer
  * indices are compile-time (PH = i mod 3) so the compiler sees that the
  * in-flight copy never aliases the tiles being read. */
-template <typename T, int D, bool CAUSAL>
-TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
+template <typename T, int D, bool CAUSAL, bool FUSED = false>
+TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr) {
   /* query rows per step: 64 at D = 64 (twice the MFMA work per barrier and
    * per softmax pass; measured 7% faster), 32 at D = 128, where 64 would not
    * fit the registers */
@@ -840,6 +840,10 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
   __shared__ __align__(1024) char lds_0[BUF];
   __shared__ __align__(1024) char lds_1[BUF];
   __shared__ __align__(1024) char lds_2[BUF];
+  /* FUSED: dS of two query blocks, [BN keys][BM queries] each, so that every
+   * wave can read all 128 keys of it (ds_off) */
+  constexpr int DS_TILE = BN * BM * 2;
+  __shared__ __align__(1024) char lds_ds[FUSED ? 2 * DS_TILE : 16];
 
   typedef typename Vec8<T>::type v8;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -882,6 +886,30 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
       kf[kt][ks] = *(const u32x4 *)(Kg + (int64_t)key * ss + ks * 32 + 8 * g);
       vf[kt][ks] = *(const u32x4 *)(Vg + (int64_t)key * ss + ks * 32 + 8 * g);
     }
+  }
+  /* FUSED: K as the B operand of dQ[:, wave's D/4 columns] = dS K, for the
+   * 128 keys in four 32-key steps; element j of a lane holds key
+   * 32 ks + 4g + j (j < 4) or 32 ks + 16 + 4g + j - 4, the order in which the
+   * transposing read of dS delivers them.  Keys at or past n are zero, so the
+   * (finite) dS of those padding keys adds nothing. */
+  constexpr int NT = FUSED ? D / 64 : 1;
+  u32x4 kq[FUSED ? 4 : 1][NT];
+  if constexpr (FUSED) {
+    const uint16_t *Kh = (const uint16_t *)Kg;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int col = wave * (D / 4) + nt * 16 + c;
+        uint32_t h[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int key = k0 + ks * 32 + (j < 4 ? 4 * g + j : 16 + 4 * g + j - 4);
+          h[j] = key < n ? Kh[(int64_t)key * ss + col] : 0u;
+        }
+        kq[ks][nt] = (u32x4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                             h[6] | (h[7] << 16)};
+      }
   }
   const float qk_scale = p.sm_scale * TM_LOG2E;
   f32x4 dk[D / 16][2], dv[D / 16][2];
@@ -963,6 +991,62 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
     }
   };
 
+  /* FUSED: byte offset of queries q .. q+3 (q a multiple of 4) of key row
+   * `key` in a dS tile; 16-byte chunks XOR-swizzled so that the 16 rows one
+   * transposing read spans fall on distinct banks */
+  auto ds_off = [&](int key, int q) {
+    constexpr int CPR = BM / 8, RP = 256 / (BM * 2);
+    return key * (BM * 2) + (((q >> 3) ^ ((key / RP) % CPR)) << 4) + (((q >> 2) & 1) << 3);
+  };
+  auto put_ds = [&](int blk, const u32x4 (&dsv)[2][KK]) {
+    char *t = lds_ds + (blk & 1) * DS_TILE;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const int key = wave * KW + kt * 16 + c;
+        *(u32x2 *)(t + ds_off(key, 32 * kk + 4 * g)) = (u32x2){dsv[kt][kk][0], dsv[kt][kk][1]};
+        *(u32x2 *)(t + ds_off(key, 32 * kk + 16 + 4 * g)) = (u32x2){dsv[kt][kk][2], dsv[kt][kk][3]};
+      }
+  };
+  /* dQ[block rows, this wave's D/4 columns] += dS K over the workgroup's 128
+   * keys, added to the fp32 accumulator with one atomic per element: the
+   * order in which workgroups reach an address varies, so dQ's rounding does */
+  auto dq_block = [&](int blk) {
+    const char *t = lds_ds + (blk & 1) * DS_TILE;
+    const int qs = q_start + blk * BM;
+    f32x4 acc[QT][NT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[qt][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const int ra = ks * 32 + 4 * g + (c >> 2), qc = qt * 16 + 4 * (c & 3);
+        const s16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4 *)(t + ds_off(ra, qc)));
+        const s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4 *)(t + ds_off(ra + 16, qc)));
+        const u32x2 ua = __builtin_bit_cast(u32x2, a0), ub = __builtin_bit_cast(u32x2, a1);
+        const v8 a = as_vec8<T>((u32x4){ua[0], ua[1], ub[0], ub[1]});
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[qt][nt] = mfma_16x16x32(a, as_vec8<T>(kq[ks][nt]), acc[qt][nt]);
+      }
+    float *dst = dq_acc + ((int64_t)bh * n + qs) * D + wave * (D / 4) + c;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = qt * 16 + 4 * g + r;
+        if (qs + row < n) {
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) unsafeAtomicAdd(dst + (int64_t)row * D + nt * 16, acc[qt][nt][r]);
+        }
+      }
+  };
+
   char *const bufs[3] = {lds_0, lds_1, lds_2};
   u32x4 pf[2][KK], dsf[2][KK]; /* P and dS of the block whose gradients are pending */
 
@@ -976,8 +1060,12 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
     char *nx2 = bufs[(PH + 2) % 3];
     if (!CHECKED || i + 2 < nblocks) stage(nx2, i + 2);
     u32x4 pf2[2][KK], ds2[2][KK];
-    if (!CHECKED || i + 1 < nblocks) scores(edge_tag, nx1, i + 1, pf2, ds2);
+    if (!CHECKED || i + 1 < nblocks) {
+      scores(edge_tag, nx1, i + 1, pf2, ds2);
+      if constexpr (FUSED) put_ds(i + 1, ds2);
+    }
     grads(cur, pf, dsf);
+    if constexpr (FUSED) dq_block(i);
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -1013,6 +1101,10 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
   wait_vmem();
   __syncthreads();
   if (nblocks > 0) scores(Edge{}, lds_0, 0, pf, dsf);
+  if constexpr (FUSED) {
+    if (nblocks > 0) put_ds(0, dsf);
+    __syncthreads();
+  }
 
   /* Block b is masked if it lies in the diagonal band (b < band) or runs past
    * n (b >= full).  Step i masks the softmax of block i+1. */
@@ -1066,7 +1158,18 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p) {
       TmAttnDkdvArgs p) {                                                                     \
     attn_dkdv_fast<T, D, CAUSAL>(p);                                                          \
   }
+/* Single-pass backward with atomic dQ (opt-in: bwd=atomic): the dK/dV
+ * kernel plus dQ = dS K per query block, and the passes around it. */
+#define TM_BWD_FUSED(T, TN, D, CAUSAL, CN)                                                    \
+  extern "C" __global__ __launch_bounds__(256) void tm_attn_fused_fast_##TN##_d##D##CN(       \
+      TmAttnFusedArgs p) {                                                                    \
+    attn_dkdv_fast<T, D, CAUSAL, true>(p.kv, p.dq_acc);                                       \
+  }
 #define TM_BWD_FAST_ALL(T, TN)           \
+  TM_BWD_FUSED(T, TN, 64, false, )       \
+  TM_BWD_FUSED(T, TN, 64, true, _causal) \
+  TM_BWD_FUSED(T, TN, 128, false, )      \
+  TM_BWD_FUSED(T, TN, 128, true, _causal) \
   TM_BWD_FAST(T, TN, 64, false, )        \
   TM_BWD_FAST(T, TN, 64, true, _causal)  \
   TM_BWD_FAST(T, TN, 128, false, )       \
@@ -1086,3 +1189,34 @@ TM_BWD_FAST_ALL(f16_t, f16)
   TM_FWD_FAST(T, TN, 128, true, _causal)
 TM_FWD_FAST_ALL(bf16_t, bf16)
 TM_FWD_FAST_ALL(f16_t, f16)
+
+/* dq_acc = 0 (count a multiple of 4), before the fused backward */
+extern "C" __global__ __launch_bounds__(256) void tm_attn_dq_acc_zero(TmAttnDqAccArgs p) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i < p.count) *(f32x4 *)(p.acc + i) = (f32x4){0.f, 0.f, 0.f, 0.f};
+}
+
+/* dq[bh, q, :] = sm_scale * dq_acc[bh, q, :] in the element type, after it:
+ * D / 8 lanes per row, 8 elements (one 16-byte store) per lane */
+template <typename T, int D>
+TM_DEV void attn_dq_convert(const TmAttnDqAccArgs &p) {
+  constexpr int LPR = D / 8, RPB = 256 / LPR;
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
+  if (row >= (int64_t)p.heads * p.n_ctx) return;
+  const int col = (threadIdx.x % LPR) * 8;
+  const int bh = (int)(row / p.n_ctx), q = (int)(row - (int64_t)bh * p.n_ctx);
+  const f32x4 a = *(const f32x4 *)(p.acc + row * D + col);
+  const f32x4 b = *(const f32x4 *)(p.acc + row * D + col + 4);
+  const float s = p.sm_scale;
+  *(u32x4 *)((T *)p.dq + (int64_t)bh * p.stride_head + (int64_t)q * p.stride_seq + col) =
+      (u32x4){pack2<T>(a[0] * s, a[1] * s), pack2<T>(a[2] * s, a[3] * s), pack2<T>(b[0] * s, b[1] * s),
+              pack2<T>(b[2] * s, b[3] * s)};
+}
+#define TM_DQ_CONVERT(T, TN, D) \
+  extern "C" __global__ __launch_bounds__(256) void tm_attn_dq_convert_##TN##_d##D(TmAttnDqAccArgs p) { \
+    attn_dq_convert<T, D>(p); \
+  }
+TM_DQ_CONVERT(bf16_t, bf16, 64)
+TM_DQ_CONVERT(bf16_t, bf16, 128)
+TM_DQ_CONVERT(f16_t, f16, 64)
+TM_DQ_CONVERT(f16_t, f16, 128)

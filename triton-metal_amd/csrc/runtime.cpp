@@ -213,10 +213,14 @@ struct BuiltinSpec {
   Element element = Element::F32;
   int head_dim = 64;
   bool causal = false;
+  /* bwd=atomic: the library also offers attn_bwd_fused, the single-pass
+   * backward whose dQ is summed with floating-point atomics (not
+   * deterministic, so never the default) */
+  bool atomic_bwd = false;
 
   std::string text() const {
-    return format("builtin element=%s head_dim=%d causal=%d", element_name(element), head_dim,
-                  causal ? 1 : 0);
+    return format("builtin element=%s head_dim=%d causal=%d%s", element_name(element), head_dim,
+                  causal ? 1 : 0, atomic_bwd ? " bwd=atomic" : "");
   }
 };
 
@@ -228,17 +232,23 @@ struct Library : Object {
   /* explicit parameters of each kernel, from the code object's metadata
    * (empty when the image carries none this library can read) */
   std::map<std::string, std::vector<tm_codeobject::ArgSlot>> signatures;
+  /* bwd=atomic: the fp32 dQ accumulator of attn_bwd_fused, grown on demand
+   * (launches of one library are ordered on its stream, so one suffices) */
+  mutable std::mutex workspace_lock;
+  mutable void *workspace = nullptr;
+  mutable size_t workspace_bytes = 0;
   ~Library() override {
-    if (!module) return;
+    if (!module && !workspace) return;
     /* a dispatch of one of its kernels may still be queued (tm_launch_async):
-     * drain the library stream before the code object goes away */
+     * drain the library stream before the code object or workspace goes away */
     Device &dev = device();
     if (dev.present) (void)hipStreamSynchronize(dev.stream);
-    (void)hipModuleUnload(module);
+    if (workspace) (void)hipFree(workspace);
+    if (module) (void)hipModuleUnload(module);
   }
 };
 
-enum class Builtin { None, Matmul, AttnFwd, AttnPre, AttnDq, AttnDkdv, SaeEncode, Probe };
+enum class Builtin { None, Matmul, AttnFwd, AttnPre, AttnDq, AttnDkdv, AttnFused, SaeEncode, Probe };
 
 struct Kernel : Object {
   Kind kind() const override { return Kind::Kernel; }
@@ -359,6 +369,10 @@ BuiltinSpec parse_spec(const char *text) {
       if (value == "0" || value == "false") spec.causal = false;
       else if (value == "1" || value == "true") spec.causal = true;
       else throw TmError("built-in library spec: causal must be 0 or 1, got '" + value + "'");
+    } else if (key == "bwd") {
+      if (value == "split") spec.atomic_bwd = false;
+      else if (value == "atomic") spec.atomic_bwd = true;
+      else throw TmError("built-in library spec: bwd must be split or atomic, got '" + value + "'");
     } else {
       throw TmError("built-in library spec: unknown key '" + key + "'");
     }
@@ -386,6 +400,10 @@ const std::vector<BuiltinInfo> &builtin_table() {
        {"E", "E", "E", "E", "E", "f32", "f32", "f32", "i32", "i32", "i32", "i32"}, 0},
       {Builtin::AttnDkdv, "attn_bwd_dkdv", {0, 0, 0, 0, 0, 0, 0, 0, 2, 1, 1, 1, 1},
        {"E", "E", "E", "E", "E", "E", "f32", "f32", "f32", "i32", "i32", "i32", "i32"}, 0},
+      /* bwd=atomic libraries only: (Q, K, V, dO, dQ, dK, dV, L, Delta, sm_scale,
+       * stride_head, stride_seq, stride_lse, n_ctx) */
+      {Builtin::AttnFused, "attn_bwd_fused", {0, 0, 0, 0, 0, 0, 0, 0, 0, 2, 1, 1, 1, 1},
+       {"E", "E", "E", "E", "E", "E", "E", "f32", "f32", "f32", "i32", "i32", "i32", "i32"}, 0},
       {Builtin::SaeEncode, "sae_encode_kernel", {0, 0, 0, 0, 1, 1, 1},
        {"E", "E", "E", "E", "i32", "i32", "i32"}, 0},
       {Builtin::Probe, "tm_probe", {0}, {"f32"}, 0},
@@ -421,6 +439,7 @@ Published published_shape(Builtin id) {
     case Builtin::AttnPre: return {256, {64}};
     case Builtin::AttnDq: return {256, {64}};
     case Builtin::AttnDkdv: return {256, {64}};
+    case Builtin::AttnFused: return {256, {128}};
     case Builtin::SaeEncode: return {256, {64, 64}}; /* SAEEncoder.swift Blocking() */
     case Builtin::Probe: return {64, {256}};
     default: return {256, {1}};
@@ -467,6 +486,9 @@ float as_f32(const Arg &a) {
 
 /* A planned dispatch: device function, geometry and the by-value argument block. */
 struct Plan {
+  /* several dispatches in order (attn_bwd_fused); the fields below are then
+   * those of the main one, for reporting */
+  std::vector<Plan> sequence;
   hipFunction_t function = nullptr;
   std::string variant;
   unsigned grid[3] = {1, 1, 1};
@@ -642,6 +664,48 @@ void choose_gemm(Plan &plan, const TmGemmArgs &p, const BuiltinSpec &spec, const
     plan.grid[1] = (unsigned)cdiv(p.n, 64);
     plan.block = 256;
   }
+}
+
+void finish(hipStream_t stream);
+
+/* attn_bwd_fused as three dispatches: clear the fp32 accumulator (a kernel,
+ * not hipMemsetAsync, so a captured graph replays it correctly), the fused
+ * dK/dV/dQ pass, then dQ = sm_scale * accumulator in the element type.
+ * `acc` holds `count` = heads * n_ctx * head_dim floats. */
+void plan_fused_backward(Plan &plan, const BuiltinSpec &spec, const TmAttnDkdvArgs &kv, void *dq,
+                         float *acc, int64_t count) {
+  const char *el = element_name(spec.element);
+  TmAttnDqAccArgs a{};
+  a.acc = acc;
+  a.dq = dq;
+  a.count = count;
+  a.sm_scale = kv.sm_scale;
+  a.stride_head = kv.stride_head;
+  a.stride_seq = kv.stride_seq;
+  a.n_ctx = kv.n_ctx;
+  a.heads = kv.heads;
+  Plan zero, main, convert;
+  zero.variant = "tm_attn_dq_acc_zero";
+  zero.grid[0] = (unsigned)cdiv(count, 1024);
+  zero.block = 256;
+  set_kernarg(zero, a);
+  TmAttnFusedArgs f{};
+  f.kv = kv;
+  f.dq_acc = acc;
+  main.variant = format("tm_attn_fused_fast_%s_d%d%s", el, spec.head_dim,
+                        spec.causal ? "_causal" : "");
+  main.grid[0] = (unsigned)(cdiv(kv.n_ctx, 128) * kv.heads);
+  main.block = 256;
+  set_kernarg(main, f);
+  convert.variant = format("tm_attn_dq_convert_%s_d%d", el, spec.head_dim);
+  convert.grid[0] = (unsigned)cdiv((int64_t)kv.heads * kv.n_ctx, 256 / (spec.head_dim / 8));
+  convert.block = 256;
+  set_kernarg(convert, a);
+  for (Plan *part : {&zero, &main, &convert}) part->function = builtin_function(part->variant);
+  plan.variant = main.variant;
+  plan.function = main.function;
+  plan.block = main.block;
+  plan.sequence = {zero, main, convert};
 }
 
 Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, int64_t gx,
@@ -884,6 +948,66 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
       }
       break;
     }
+    case Builtin::AttnFused: {
+      const char *nm = info.name;
+      const float sm_scale = as_f32(args[9]);
+      TmAttnDkdvArgs kv{};
+      kv.stride_head = as_i32(args[10]);
+      kv.stride_seq = as_i32(args[11]);
+      kv.stride_lse = as_i32(args[12]);
+      kv.n_ctx = as_i32(args[13]);
+      validate_attn_common(nm, heads, kv.stride_head, kv.stride_seq, kv.n_ctx, spec.head_dim);
+      require_nonneg(kv.stride_lse, nm, "stride_lse");
+      const int64_t ext = heads > 0 && kv.n_ctx > 0
+                              ? sat_add((heads - 1) * (int64_t)kv.stride_head,
+                                    extent(kv.n_ctx, kv.stride_seq, spec.head_dim, 1))
+                              : 0;
+      for (int i = 0; i < 7; ++i) require_extent(args[i], ext, es, nm, i, "tensor");
+      const int64_t sext =
+          heads > 0 && kv.n_ctx > 0 ? (heads - 1) * (int64_t)kv.stride_lse + kv.n_ctx : 0;
+      require_extent(args[7], sext, 4, nm, 7, "L");
+      require_extent(args[8], sext, 4, nm, 8, "Delta");
+      if (kv.n_ctx == 0 || heads == 0) {
+        plan.empty = true;
+        return plan;
+      }
+      if (!attn_fast_ok(spec, kv.stride_head, kv.stride_seq, kv.n_ctx, sm_scale))
+        throw TmError(format("%s runs only on the specialised path: 16-bit elements, head_dim 64 "
+                             "or 128, strides multiples of 8, a positive finite sm_scale and "
+                             "heads under 2 GiB",
+                             nm));
+      kv.q = args[0].buffer->ptr;
+      kv.k = args[1].buffer->ptr;
+      kv.v = args[2].buffer->ptr;
+      kv.dout = args[3].buffer->ptr;
+      kv.dk = args[5].buffer->ptr;
+      kv.dv = args[6].buffer->ptr;
+      kv.lse = (const float *)args[7].buffer->ptr;
+      kv.delta = (const float *)args[8].buffer->ptr;
+      kv.sm_scale = sm_scale;
+      kv.head_dim = spec.head_dim;
+      kv.heads = (int32_t)heads;
+      const int64_t count = heads * kv.n_ctx * (int64_t)spec.head_dim;
+      float *acc = nullptr;
+      {
+        std::lock_guard<std::mutex> guard(lib.workspace_lock);
+        const size_t need = (size_t)count * sizeof(float);
+        if (lib.workspace_bytes < need) {
+          /* the old accumulator may still be bound to a queued dispatch */
+          if (lib.workspace) {
+            finish(require_device().stream);
+            hip_check(hipFree(lib.workspace), "hipFree");
+            lib.workspace = nullptr;
+            lib.workspace_bytes = 0;
+          }
+          hip_check(hipMalloc(&lib.workspace, need), "hipMalloc (dQ accumulator)");
+          lib.workspace_bytes = need;
+        }
+        acc = (float *)lib.workspace;
+      }
+      plan_fused_backward(plan, spec, kv, args[4].buffer->ptr, acc, count);
+      return plan;
+    }
     case Builtin::Probe: {
       require_extent(args[0], 256, 4, info.name, 0, "out");
       void *out = args[0].buffer->ptr;
@@ -1017,6 +1141,10 @@ int64_t max_threads(Kernel &k) {
 
 void enqueue(const Plan &plan, hipStream_t stream) {
   if (plan.empty) return;
+  if (!plan.sequence.empty()) {
+    for (const Plan &part : plan.sequence) enqueue(part, stream);
+    return;
+  }
   if (!plan.function || plan.block == 0 || plan.block > 1024 || !plan.grid[0] || !plan.grid[1] ||
       !plan.grid[2])
     throw TmError("internal error: dispatch of '" + plan.variant +
@@ -1202,6 +1330,7 @@ std::string kernel_info_json(const BuiltinSpec &spec) {
   out << "{\n  \"kernels\" : [\n";
   bool first = true;
   for (const BuiltinInfo &info : builtin_table()) {
+    if (info.id == Builtin::AttnFused && !spec.atomic_bwd) continue;
     const Published pub = published_shape(info.id);
     if (!first) out << ",\n";
     first = false;
@@ -1346,6 +1475,10 @@ int64_t tm_load_kernel(int64_t library, const char *name) {
     if (!info)
       throw TmError(format("kernel '%s' not found in library (available: %s)", name,
                            builtin_names().c_str()));
+    if (info->id == Builtin::AttnFused && !lib->spec.atomic_bwd)
+      throw TmError("kernel 'attn_bwd_fused' is offered only by built-in libraries whose spec "
+                    "has bwd=atomic (its dQ is summed with floating-point atomics, so it is not "
+                    "deterministic)");
     k->builtin = info->id;
   } else {
     hipError_t status = hipModuleGetFunction(&k->function, lib->module, name);

@@ -73,4 +73,23 @@ struct TmAttnDkdvArgs {
   int32_t head_dim, heads;
 };
 
+/* attn_bwd_fused (built-in libraries with bwd=atomic; no reference kernel —
+ * the variant the reference names at AttentionBackwardKernel.swift:27-41 and
+ * docs/COMPARISON.md:151-154): the dK/dV kernel's arguments plus dQ and its
+ * fp32 accumulator, [heads][n_ctx][head_dim] dense, zeroed before the launch. */
+struct TmAttnFusedArgs {
+  TmAttnDkdvArgs kv;
+  float *dq_acc;
+};
+
+/* The passes around attn_bwd_fused: clear dq_acc (count floats), then write
+ * dq = sm_scale * dq_acc in the element type at the caller's strides. */
+struct TmAttnDqAccArgs {
+  float *acc;
+  void *dq;
+  int64_t count;
+  float sm_scale;
+  int32_t stride_head, stride_seq, n_ctx, heads;
+};
+
 #endif

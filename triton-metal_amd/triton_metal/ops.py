@@ -31,22 +31,28 @@ def cdiv(a, b):
 
 
 class BuiltinLibrary:
-    """One built-in library spec and its five kernels, loaded once."""
+    """One built-in library spec and its kernels, loaded once.  bwd="atomic"
+    adds attn_bwd_fused, the single-pass backward with an atomically summed
+    (non-deterministic) dQ."""
 
     NAMES = ("matmul_kernel", "attn_fwd", "attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv",
              "sae_encode_kernel")
 
-    def __init__(self, element="f32", head_dim=64, causal=False):
+    def __init__(self, element="f32", head_dim=64, causal=False, bwd="split"):
         if element not in _ELEMENTS:
             raise ValueError(f"element must be one of {sorted(_ELEMENTS)}")
+        if bwd not in ("split", "atomic"):
+            raise ValueError("bwd must be 'split' or 'atomic'")
         self.element = element
         self.dtype = _ELEMENTS[element]
         self.head_dim = head_dim
         self.causal = causal
-        self.spec = f"builtin element={element} head_dim={head_dim} causal={int(causal)}"
+        self.bwd = bwd
+        self.spec = f"builtin element={element} head_dim={head_dim} causal={int(causal)} bwd={bwd}"
         self.info = {k["name"]: k for k in json.loads(_core.kernel_info(self.spec))["kernels"]}
         self.handle = _core.compile_msl(self.spec)
-        self.kernels = {name: _core.load_kernel(self.handle, name) for name in self.NAMES}
+        names = self.NAMES + (("attn_bwd_fused",) if bwd == "atomic" else ())
+        self.kernels = {name: _core.load_kernel(self.handle, name) for name in names}
 
     def release(self):
         for handle in self.kernels.values():
@@ -60,10 +66,10 @@ class BuiltinLibrary:
 _CACHE = {}
 
 
-def library(element="f32", head_dim=64, causal=False) -> BuiltinLibrary:
-    key = (element, head_dim, bool(causal))
+def library(element="f32", head_dim=64, causal=False, bwd="split") -> BuiltinLibrary:
+    key = (element, head_dim, bool(causal), bwd)
     if key not in _CACHE:
-        _CACHE[key] = BuiltinLibrary(element, head_dim, causal)
+        _CACHE[key] = BuiltinLibrary(element, head_dim, causal, bwd)
     return _CACHE[key]
 
 
@@ -199,6 +205,8 @@ class AttentionLayer:
 
     `heads` is batch*heads: the reference's layout [B*H, S, D] with
     stride_head = S*D and stride_seq = D (AttentionKernel.swift:25-28).
+    bwd="atomic" runs the backward as preprocess + attn_bwd_fused instead of
+    preprocess + dq + dkdv.
     """
 
     #: per-(head, row) tensors: the forward's L (log2 units) and the backward's Delta
@@ -207,14 +215,15 @@ class AttentionLayer:
     TENSORS = ("q", "k", "v", "o", "do", "dq", "dk", "dv")
 
     def __init__(self, heads, seq, dim, element="f32", causal=False, scale=None,
-                 block_m=16, block_n=32):
+                 block_m=16, block_n=32, bwd="split"):
         self.heads, self.seq, self.dim = heads, seq, dim
         self.element, self.causal = element, causal
         # the reference caller's tile sizes only shape the requested grids; the
         # library covers the problem with its own tiles
         self.block_m, self.block_n = block_m, block_n
         self.scale = scale if scale is not None else 1.0 / math.sqrt(dim)
-        self.lib = library(element, dim, causal)
+        self.bwd = bwd
+        self.lib = library(element, dim, causal, bwd)
         self.buffers = {}
         for name in self.TENSORS:
             self.buffers[name] = DeviceBuffer((heads, seq, dim), _ELEMENTS[element])
@@ -274,6 +283,14 @@ class AttentionLayer:
             _core.float_bits(self.scale), self.seq * self.dim, self.dim, self.seq, self.seq]
         return grid, kinds, values
 
+    def fused_args(self):
+        B, I, F = _core.ARG_BUFFER, _core.ARG_I32, _core.ARG_F32
+        grid = (cdiv(self.seq, self.block_n), self.heads, 1)
+        kinds = [B] * 9 + [F, I, I, I, I]
+        values = [self._h(x) for x in ("q", "k", "v", "do", "dq", "dk", "dv", "lse", "delta")] + [
+            _core.float_bits(self.scale), self.seq * self.dim, self.dim, self.seq, self.seq]
+        return grid, kinds, values
+
     # -- passes --------------------------------------------------------------
 
     def run_forward(self, synchronous=True, stats=True):
@@ -282,6 +299,9 @@ class AttentionLayer:
     def run_backward(self, synchronous=True):
         k = self.lib.kernels
         _go(k["attn_bwd_preprocess"], *self.pre_args(), synchronous=False)
+        if self.bwd == "atomic":
+            _go(k["attn_bwd_fused"], *self.fused_args(), synchronous=synchronous)
+            return
         _go(k["attn_bwd_dq"], *self.dq_args(), synchronous=False)
         _go(k["attn_bwd_dkdv"], *self.dkdv_args(), synchronous=synchronous)
 
