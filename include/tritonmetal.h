@@ -143,6 +143,18 @@ int32_t tm_synchronize(void);
 int32_t tm_launch_timed(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads,
                         const int32_t *kinds, const int64_t *values, int32_t argc,
                         int32_t repeats, float *elapsed_ms);
+/* tm_launch that allocates nothing.  No reference counterpart: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  A dispatch that needs a work buffer
+ * (attn_bwd_fused's fp32 dQ accumulator, heads * n_ctx * head_dim * 4 bytes)
+ * takes it from a static device array of 64 MiB per device, held from the
+ * first such call until the process ends; larger requests are refused with an
+ * error (use tm_launch).  The caller passes inputs and outputs as for
+ * tm_launch; this call waits.  Calls in one process are serialised on a lock;
+ * the array keeps the last call's contents, and every dispatch clears what it
+ * needs zeroed.  0 / -1. */
+int32_t tm_launch_noalloc(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads,
+                          const int32_t *kinds, const int64_t *values, int32_t argc);
 /* Name of the device function the last planned dispatch of `kernel` ran (the
  * symbol rocprof reports), NULL on failure.  For tests and profiling. */
 char *tm_kernel_variant(int64_t kernel);

@@ -29,7 +29,7 @@ def test_library_is_the_in_tree_build(core):
 
 def test_every_declared_export_is_present(core):
     names = declared_exports()
-    assert len(names) == 27
+    assert len(names) == 28
     for name in names:
         assert hasattr(core._lib, name), name
     # The reference's 23 exports are all declared.

@@ -5,7 +5,10 @@
 Steps:
   1. every csrc/kernels/*.hip -> lib/<name>.hsaco  (hipcc --genco, gfx950);
   2. lib/blobs.S: a table linking those images into the library;
-  3. csrc/runtime.cpp + lib/blobs.S -> lib/libtritonmetal.so  (the tm_* C ABI).
+  3. csrc/scratch.hip -> lib/scratch.o  (the static device scratch of
+     tm_launch_noalloc; hipcc, host and gfx950 device code);
+  4. csrc/runtime.cpp + lib/blobs.S + lib/scratch.o -> lib/libtritonmetal.so
+     (the tm_* C ABI).
 
 Outputs stay in lib/ (git-ignored, shipped with the tree).  Compiler flags:
 -O3, gfx950 only, packed-fp32 instruction selection disabled (the kernels are
@@ -72,20 +75,26 @@ def write_blobs(images):
     return path
 
 
+def build_scratch() -> Path:
+    out = LIB / "scratch.o"
+    _run([HIPCC, *HIP_FLAGS, "-fPIC", "-c", str(CSRC / "scratch.hip"), "-o", str(out)])
+    return out
+
+
 def build_sanitized() -> Path:
     """The host library alone (runtime + code-object reader, kernels as built)
     under AddressSanitizer and UndefinedBehaviorSanitizer, for CPU test runs:
         LD_PRELOAD="$(gcc -print-file-name=libasan.so) $(gcc -print-file-name=libubsan.so)" \\
         ASAN_OPTIONS=detect_leaks=0 TRITON_METAL_CORE_LIB=<this file> pytest tests -m "not gpu"
     Host code only: the kernels are the normal gfx950 builds."""
-    blobs = LIB / "blobs.S"
-    if not blobs.exists():
+    blobs, scratch = LIB / "blobs.S", LIB / "scratch.o"
+    if not blobs.exists() or not scratch.exists():
         build()
     out = LIB / "libtritonmetal_asan.so"
     _run([
         "g++", "-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
         "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}",
-        str(CSRC / "runtime.cpp"), str(CSRC / "codeobject.cpp"), str(blobs),
+        str(CSRC / "runtime.cpp"), str(CSRC / "codeobject.cpp"), str(blobs), str(scratch),
         "-o", str(out),
         f"-L{ROCM / 'lib'}", "-lamdhip64", "-lhiprtc", f"-Wl,-rpath,{ROCM / 'lib'}",
     ])
@@ -96,12 +105,14 @@ def build(jobs: int = 8) -> Path:
     LIB.mkdir(exist_ok=True)
     srcs = kernel_sources()
     with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
+        scratch_job = pool.submit(build_scratch)
         images = list(pool.map(build_kernel, srcs))
+        scratch = scratch_job.result()
     blobs = write_blobs(images)
     _run([
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
         "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}",
-        str(CSRC / "runtime.cpp"), str(CSRC / "codeobject.cpp"), str(blobs),
+        str(CSRC / "runtime.cpp"), str(CSRC / "codeobject.cpp"), str(blobs), str(scratch),
         "-o", str(LIBRARY),
         f"-L{ROCM / 'lib'}", "-lamdhip64", "-lhiprtc", f"-Wl,-rpath,{ROCM / 'lib'}",
     ])

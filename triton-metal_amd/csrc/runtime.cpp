@@ -41,6 +41,7 @@
 #include <vector>
 
 #include "codeobject.h"
+#include "scratch.h"
 #include "tm_args.h"
 
 /* Query rows and threads per workgroup of the specialised forward kernels
@@ -163,18 +164,22 @@ BuiltinModules &builtin_modules() {
   return mods;
 }
 
+/* Load the built-in kernel images once (caller holds mods.lock). */
+void load_builtin_modules(BuiltinModules &mods) {
+  if (!mods.modules.empty()) return;
+  for (int i = 0; i < tm_builtin_blob_count; ++i) {
+    hipModule_t mod;
+    hip_check(hipModuleLoadData(&mod, tm_builtin_blob_table[i].start),
+              "hipModuleLoadData (built-in kernels)");
+    mods.modules.push_back(mod);
+  }
+}
+
 hipFunction_t builtin_function(const std::string &symbol) {
   require_device();
   BuiltinModules &mods = builtin_modules();
   std::lock_guard<std::mutex> guard(mods.lock);
-  if (mods.modules.empty()) {
-    for (int i = 0; i < tm_builtin_blob_count; ++i) {
-      hipModule_t mod;
-      hip_check(hipModuleLoadData(&mod, tm_builtin_blob_table[i].start),
-                "hipModuleLoadData (built-in kernels)");
-      mods.modules.push_back(mod);
-    }
-  }
+  load_builtin_modules(mods);
   auto it = mods.functions.find(symbol);
   if (it != mods.functions.end()) return it->second;
   for (hipModule_t mod : mods.modules) {
@@ -708,8 +713,15 @@ void plan_fused_backward(Plan &plan, const BuiltinSpec &spec, const TmAttnDkdvAr
   plan.sequence = {zero, main, convert};
 }
 
+/* Device memory a planned dispatch may use instead of allocating its own work
+ * buffer: tm_launch_noalloc passes the static scratch (scratch.hip). */
+struct Scratch {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+
 Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, int64_t gx,
-                  int64_t gy, int64_t gz) {
+                  int64_t gy, int64_t gz, const Scratch *scratch = nullptr) {
   const BuiltinInfo &info = *find_builtin(k.name);
   check_signature(info, args);
   const BuiltinSpec &spec = lib.spec;
@@ -989,7 +1001,15 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
       kv.heads = (int32_t)heads;
       const int64_t count = heads * kv.n_ctx * (int64_t)spec.head_dim;
       float *acc = nullptr;
-      {
+      if (scratch) {
+        const size_t need = (size_t)count * sizeof(float);
+        if (need > scratch->bytes)
+          throw TmError(format("%s through tm_launch_noalloc needs a %zu-byte dQ accumulator "
+                               "(heads * n_ctx * head_dim * 4) but the static scratch holds %zu "
+                               "bytes; launch it with tm_launch",
+                               nm, need, scratch->bytes));
+        acc = (float *)scratch->ptr;
+      } else {
         std::lock_guard<std::mutex> guard(lib.workspace_lock);
         const size_t need = (size_t)count * sizeof(float);
         if (lib.workspace_bytes < need) {
@@ -1171,7 +1191,8 @@ void enqueue(const Plan &plan, hipStream_t stream) {
 Plan prepare(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads,
              const int32_t *kinds, const int64_t *values, int32_t argc,
              std::shared_ptr<Kernel> &k_out,
-             std::vector<std::shared_ptr<Buffer>> *mirrored = nullptr) {
+             std::vector<std::shared_ptr<Buffer>> *mirrored = nullptr,
+             const Scratch *scratch = nullptr) {
   auto k = handles().lookup<Kernel>(kernel, Kind::Kernel, "kernel");
   k_out = k;
   std::vector<Arg> args = decode_args(kinds, values, argc);
@@ -1194,7 +1215,7 @@ Plan prepare(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads
                          (long long)threads, (long long)limit));
   Plan plan;
   if (k->builtin != Builtin::None) {
-    plan = plan_builtin(*k, *k->library, args, gx, gy, gz);
+    plan = plan_builtin(*k, *k->library, args, gx, gy, gz, scratch);
   } else {
     require_device();
     const int64_t user_limit = max_threads(*k);
@@ -1281,10 +1302,10 @@ std::vector<char> compile_hip_source(const char *source) {
 
 int64_t launch_common(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads,
                       const int32_t *kinds, const int64_t *values, int32_t argc, bool wait,
-                      int32_t repeats, float *elapsed_ms) {
+                      int32_t repeats, float *elapsed_ms, const Scratch *scratch = nullptr) {
   std::shared_ptr<Kernel> k;
   std::vector<std::shared_ptr<Buffer>> mirrored;
-  Plan plan = prepare(kernel, gx, gy, gz, threads, kinds, values, argc, k, &mirrored);
+  Plan plan = prepare(kernel, gx, gy, gz, threads, kinds, values, argc, k, &mirrored, scratch);
   Device &dev = require_device();
   /* buffers with a host mirror: mirror -> HBM before, HBM -> mirror after */
   for (const auto &b : mirrored) {
@@ -1480,6 +1501,17 @@ int64_t tm_load_kernel(int64_t library, const char *name) {
                     "has bwd=atomic (its dQ is summed with floating-point atomics, so it is not "
                     "deterministic)");
     k->builtin = info->id;
+    /* load the kernel images now, so that launches (tm_launch_noalloc among
+     * them) load no code; a failure here resurfaces at the first launch */
+    if (device().present) {
+      BuiltinModules &mods = builtin_modules();
+      std::lock_guard<std::mutex> guard(mods.lock);
+      try {
+        load_builtin_modules(mods);
+      } catch (const TmError &) {
+        (void)hipGetLastError();
+      }
+    }
   } else {
     hipError_t status = hipModuleGetFunction(&k->function, lib->module, name);
     if (status != hipSuccess) {
@@ -1643,6 +1675,25 @@ int32_t tm_launch_timed(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int6
   if (!elapsed_ms) throw TmError("tm_launch_timed received a NULL elapsed_ms");
   return (int32_t)launch_common(kernel, gx, gy, gz, threads, kinds, values, argc, true, repeats,
                                 elapsed_ms);
+  TM_GUARD_END(-1)
+}
+
+/* tm_launch with no allocation: a dispatch that needs a work buffer takes it
+ * from the static scratch (scratch.hip) instead of library-owned memory.
+ * One lock holds from planning to the wait, so this process's calls never
+ * overlap on the scratch; it keeps the last call's contents, and each
+ * dispatch clears what it needs zeroed with a kernel. */
+int32_t tm_launch_noalloc(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads,
+                          const int32_t *kinds, const int64_t *values, int32_t argc) {
+  TM_GUARD_BEGIN
+  static std::mutex noalloc_lock;
+  std::lock_guard<std::mutex> guard(noalloc_lock);
+  require_device();
+  Scratch scratch;
+  hip_check(tm_scratch_address(&scratch.ptr), "hipGetSymbolAddress (static scratch)");
+  scratch.bytes = TM_SCRATCH_BYTES;
+  return (int32_t)launch_common(kernel, gx, gy, gz, threads, kinds, values, argc, true, 0,
+                                nullptr, &scratch);
   TM_GUARD_END(-1)
 }
 

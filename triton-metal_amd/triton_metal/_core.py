@@ -81,6 +81,10 @@ _SIGNATURES = {
          _i32, ctypes.POINTER(ctypes.c_float)],
     ),
     "tm_kernel_variant": (_ptr, [_i64]),
+    "tm_launch_noalloc": (
+        _i32,
+        [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_i32), ctypes.POINTER(_i64), _i32],
+    ),
 }
 
 #: The exports the reference's C ABI has (reference _core.py:70-100).
@@ -243,6 +247,17 @@ def launch_async(kernel, grid, threads_per_threadgroup, kinds, values) -> None:
     _check(
         _lib.tm_launch_async(kernel, grid[0], grid[1], grid[2], threads_per_threadgroup,
                              kind_array, value_array, count),
+        -1,
+    )
+
+
+def launch_noalloc(kernel, grid, threads_per_threadgroup, kinds, values) -> None:
+    """launch() that allocates no device memory: a work buffer comes from the
+    library's static device scratch (64 MiB); larger requests raise."""
+    kind_array, value_array, count = _arrays(kinds, values)
+    _check(
+        _lib.tm_launch_noalloc(kernel, grid[0], grid[1], grid[2], threads_per_threadgroup,
+                               kind_array, value_array, count),
         -1,
     )
 
