@@ -56,6 +56,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the baseline sample")
     ap.add_argument("--only", choices=["all", "fa", "gemm", "reference"], default="all")
+    ap.add_argument("--vendor", action="store_true",
+                    help="time the vendor libraries on the same shapes (torch.matmul = hipBLASLt at "
+                         "config 3; torch scaled_dot_product_attention, each ROCm backend, at "
+                         "config 5) as one JSON line and exit; a comparison, not a baseline")
     ap.add_argument("--probes", action="store_true",
                     help="print the device probe rates (MFMA shapes, exp2, LDS reads, fp32 atomics) "
                          "as one JSON line and exit")
@@ -118,6 +122,60 @@ def profile_pass(core, ops):
     for t in (x, w, bias, out):
         t.free()
     print(json.dumps({"profile_pass": "done", "copy_bytes": COPY_BYTES}), flush=True)
+
+
+def vendor_reference():
+    """torch's own kernels on this GPU at the headline shapes: hipBLASLt through
+    torch.matmul (bf16 8192^3) and scaled_dot_product_attention (B4 H32 S4096
+    D128 bf16 causal, forward and backward) under each backend torch offers on
+    ROCm.  CUDA-event timing of back-to-back calls after a warm-up."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    def timed(fn, n, warm):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(n):
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / n
+
+    out = {"torch": torch.__version__}
+    n = 8192
+    a = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    ms = timed(lambda: a @ b, 20, 5)
+    out["matmul_bf16_8192"] = {"ms": round(ms, 4), "tflops": round(gemm_flops(n, n, n) / ms / 1e9, 1)}
+    del a, b
+    B, H, S, D = 4, 32, 4096, 128
+    q, k, v = (torch.randn(B, H, S, D, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+               for _ in range(3))
+    d_out = torch.randn(B, H, S, D, device="cuda", dtype=torch.bfloat16)
+    f_fwd = attention_flops(B * H, S, D, True)
+    f_bwd = attention_flops(B * H, S, D, True, backward=True)
+    for name, backend in (("flash", SDPBackend.FLASH_ATTENTION),
+                          ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel(backend):
+                fwd = lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True)
+                ms_f = timed(fwd, 10, 3)
+                o = fwd()
+
+                def bwd():
+                    q.grad = k.grad = v.grad = None
+                    o.backward(d_out, retain_graph=True)
+                ms_b = timed(bwd, 10, 3)
+            out[f"sdpa_{name}_config5"] = {
+                "fwd_ms": round(ms_f, 4), "fwd_tflops": round(f_fwd / ms_f / 1e9, 1),
+                "bwd_ms": round(ms_b, 4), "bwd_tflops": round(f_bwd / ms_b / 1e9, 1)}
+        except RuntimeError as e:  # a backend this torch build lacks
+            out[f"sdpa_{name}_config5"] = {"unavailable": str(e)[:200]}
+    return out
 
 
 def normal_bf16(shape, seed):
@@ -372,6 +430,10 @@ def main():
               "shards over batch*heads with no communication).", file=sys.stderr)
         sys.exit(2)
 
+    if args.vendor:
+        # before this library touches the device: torch initialises HIP itself
+        print(json.dumps({"vendor": vendor_reference()}))
+        return
     from triton_metal import _core as core
     from triton_metal import ops
 
