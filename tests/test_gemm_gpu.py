@@ -229,7 +229,8 @@ def test_large_aligned_gemm_hybrid_and_checksums(device, element):
 def test_config3_bf16_8192_cube(device):
     """Config 3: bf16 8192^3, N(0,1) from seed, f32 accumulate, bf16 out.
     Full size: 256 sampled rows against fp64 (from the bf16-rounded inputs) under
-    the 2e-2 hybrid metric, and the column-sum checksum over all rows."""
+    the 2e-2 hybrid metric, the column-sum checksum over all rows, and every
+    element against an fp32 BLAS product under the same metric."""
     m = n = k = 8192
     a = round_to(G.normal((m, k), seed=0), "bf16")
     b = round_to(G.normal((k, n), seed=1), "bf16")
@@ -242,3 +243,11 @@ def test_config3_bf16_8192_cube(device):
     print(f"config3 variant={variant} hybrid={err:.3e} max_abs={T.max_abs_error(c[rows], want):.3e}")
     assert err <= 2e-2
     _assert_column_checksum(a, b, c, "bf16")
+    # every element: against an fp32 BLAS product of the same rounded inputs
+    # (bf16 products are exact in fp32; its own summation error, measured on
+    # the sampled rows against fp64, is a few units of 2^-24 relative)
+    want32 = a @ b
+    assert T.hybrid_error(want32[rows], want) <= 1e-4
+    err_all = T.hybrid_error(c, want32)
+    print(f"config3 all rows vs fp32 BLAS: hybrid={err_all:.3e}")
+    assert err_all <= 2e-2
