@@ -211,7 +211,7 @@ def bench_attention(core, ops, batch, heads, seq, dim, causal, steps, warmup, sa
             layer.buffers[name].write(x)
         kern = layer.lib.kernels
         launches = [("attn_fwd", layer.fwd_args(True))]
-        if backward and bwd == "atomic":
+        if backward and bwd != "split":
             launches += [("attn_bwd_preprocess", layer.pre_args()),
                          ("attn_bwd_fused", layer.fused_args())]
         elif backward:
@@ -505,6 +505,16 @@ def main():
             "frac_of_peak": round(f_bwd / (ms_a * 1e-3) / 1e12 / 2500, 4),
             "ms": round(ms_a, 4), "fused_ms": round(ka["attn_bwd_fused"]["ms"], 4),
             "vs_split": round(bwd_ms / ms_a, 3), "variant": ka["attn_bwd_fused"]["variant"]}
+        # the deterministic one-call backward (bwd=stash: dK/dV kernel keeps dS
+        # for a dQ kernel, no recomputation), beside the split as well
+        _, ks = bench_attention(core, ops, B, H, S, D, True, 0, args.warmup, args.sample_ms,
+                                bwd="stash")
+        ms_s = ks["attn_bwd_preprocess"]["ms"] + ks["attn_bwd_fused"]["ms"]
+        components["fa2_bwd_stash"] = {
+            "tflops": round(f_bwd / (ms_s * 1e-3) / 1e12, 2),
+            "frac_of_peak": round(f_bwd / (ms_s * 1e-3) / 1e12 / 2500, 4),
+            "ms": round(ms_s, 4), "fused_ms": round(ks["attn_bwd_fused"]["ms"], 4),
+            "vs_split": round(bwd_ms / ms_s, 3), "variant": ks["attn_bwd_fused"]["variant"]}
         # fp16 variant of config 5 (the reference's own attention element type)
         _, k16 = bench_attention(core, ops, B, H, S, D, True, 0, args.warmup, args.sample_ms,
                                  element="f16")

@@ -18,15 +18,15 @@
  *       * a gfx950 code object image (tm_load_metallib),
  *       * HIP C++ source compiled at run time by hiprtc (tm_compile_msl), or
  *       * a built-in library spec "builtin [element=f32|f16|bf16]
- *         [head_dim=N] [causal=0|1] [bwd=split|atomic]" (tm_compile_msl),
+ *         [head_dim=N] [causal=0|1] [bwd=split|atomic|stash]" (tm_compile_msl),
  *         which names the library's hand-written gfx950 kernels for the dense
  *         hot path: matmul_kernel, attn_fwd, attn_bwd_preprocess, attn_bwd_dq,
  *         attn_bwd_dkdv, sae_encode_kernel (relu(x @ W + b),
  *         Sources/TritonMetalMLX/SAEEncoder.swift:29-40), tm_probe, and with
- *         bwd=atomic attn_bwd_fused (the single-pass backward with an
- *         atomically summed dQ that AttentionBackwardKernel.swift:27-41
- *         names: Q, K, V, dO, dQ, dK, dV, L, Delta, sm_scale, stride_head,
- *         stride_seq, stride_lse, n_ctx).
+ *         bwd=atomic or bwd=stash attn_bwd_fused (the backward in one call
+ *         that AttentionBackwardKernel.swift:27-41 names: Q, K, V, dO, dQ, dK,
+ *         dV, L, Delta, sm_scale, stride_head, stride_seq, stride_lse, n_ctx;
+ *         atomic sums dQ with fp32 atomics, stash keeps dS for a dQ pass).
  *   - a "buffer" is device memory in HBM (hipMalloc).  tm_buffer_contents
  *     gives it a host-addressable mirror (pinned host memory) that stands in
  *     for the reference's unified memory: while the mirror exists, host
@@ -146,7 +146,8 @@ int32_t tm_launch_timed(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int6
 /* tm_launch that allocates nothing.  No reference counterpart: for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  A dispatch that needs a work buffer
- * (attn_bwd_fused's fp32 dQ accumulator, heads * n_ctx * head_dim * 4 bytes)
+ * (attn_bwd_fused's fp32 dQ accumulator under bwd=atomic, heads * n_ctx *
+ * head_dim * 4 bytes, or its dS stash under bwd=stash, about heads * n_ctx^2 * 2)
  * takes it from a static device array of 64 MiB per device, held from the
  * first such call until the process ends; larger requests are refused with an
  * error (use tm_launch).  The caller passes inputs and outputs as for

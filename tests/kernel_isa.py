@@ -83,15 +83,29 @@ def is_lds_dma(mnemonic: str, operands: str) -> bool:
     return mnemonic.startswith("buffer_load_") and re.search(r"\blds\b", operands) is not None
 
 
-def waits_all_vmem(mnemonic: str, operands: str) -> bool:
-    return mnemonic == "s_waitcnt" and "vmcnt(0)" in operands
+def is_vmem(mnemonic: str) -> bool:
+    return mnemonic.startswith(("buffer_", "global_", "flat_", "scratch_"))
 
 
-def barriers_with_copy_in_flight(insns):
+def vmcnt_wait(mnemonic: str, operands: str):
+    """N of an `s_waitcnt vmcnt(N)`, or None."""
+    if mnemonic != "s_waitcnt":
+        return None
+    m = re.search(r"vmcnt\((\d+)\)", operands)
+    return int(m.group(1)) if m else None
+
+
+def barriers_with_copy_in_flight(insns, depth=0):
     """Dataflow over the kernel's control-flow graph: the s_barrier
-    instructions that some path reaches with an LDS copy issued and no
-    vmcnt(0) wait since.  Such a barrier would release the workgroup before
-    this wave's part of a tile has landed."""
+    instructions that some path reaches with an LDS copy that no vmcnt wait
+    has covered and that has already crossed `depth` barriers.  vmcnt counts
+    vector memory instructions in issue order, so `s_waitcnt vmcnt(N)` covers
+    every copy followed by at least N later vector memory instructions.
+    depth 0: every copy lands before the next barrier (a tile is published by
+    the barrier after its copy); depth 1: before the second (three buffers in
+    rotation, the copy of block j+2 in flight while block j is computed).  A
+    violation would let a workgroup read a tile before this wave's part of it
+    has landed."""
     if not insns:
         return []
     addrs = [a for a, *_ in insns]
@@ -116,30 +130,47 @@ def barriers_with_copy_in_flight(insns):
         if mn != "s_endpgm" and not mn.startswith("s_branch") and e < len(insns):
             out.append(block_of[e])
         succ.append(out)
-    pending_in = [False] * len(blocks)
+
+    # state: a tuple over the copies that crossed 0, 1, ... depth barriers;
+    # each entry None (no uncovered copy) or the fewest vector memory
+    # instructions issued after the newest uncovered copy of that group
+    def bump(k):
+        return None if k is None else k + 1
+
+    def step(state, mn, ops):
+        if is_lds_dma(mn, ops):
+            return (0,) + tuple(bump(k) for k in state[1:])
+        if is_vmem(mn):
+            return tuple(bump(k) for k in state)
+        n = vmcnt_wait(mn, ops)
+        if n is not None:
+            return tuple(None if (k is not None and k >= n) else k for k in state)
+        if mn == "s_barrier":
+            return (None,) + state[:-1]
+        return state
+
+    def meet(x, y):
+        return tuple(a if b is None else b if a is None else min(a, b) for a, b in zip(x, y))
+
+    empty = (None,) * (depth + 1)
+    state_in = [empty] * len(blocks)
     changed = True
     while changed:
         changed = False
         for k, (s, e) in enumerate(blocks):
-            p = pending_in[k]
+            st = state_in[k]
             for a, mn, ops, tgt in insns[s:e]:
-                if is_lds_dma(mn, ops):
-                    p = True
-                elif waits_all_vmem(mn, ops):
-                    p = False
+                st = step(st, mn, ops)
             for nk in succ[k]:
-                if p and not pending_in[nk]:
-                    pending_in[nk] = True
+                new = meet(state_in[nk], st)
+                if new != state_in[nk]:
+                    state_in[nk] = new
                     changed = True
     bad = []
     for k, (s, e) in enumerate(blocks):
-        p = pending_in[k]
+        st = state_in[k]
         for a, mn, ops, tgt in insns[s:e]:
-            if is_lds_dma(mn, ops):
-                p = True
-            elif waits_all_vmem(mn, ops):
-                p = False
-            elif mn == "s_barrier" and p:
+            if mn == "s_barrier" and st[-1] is not None:
                 bad.append(a)
+            st = step(st, mn, ops)
     return bad
-

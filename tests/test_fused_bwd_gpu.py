@@ -1,17 +1,20 @@
-"""The opt-in single-pass backward (built-in spec bwd=atomic, kernel
-attn_bwd_fused): dK and dV from the same arithmetic as attn_bwd_dkdv, dQ
-accumulated across key blocks with fp32 atomics.
+"""The opt-in backward in one call (kernel attn_bwd_fused), in its two forms:
+  bwd=atomic  dK and dV from the same arithmetic as attn_bwd_dkdv, dQ
+              accumulated across key blocks with fp32 atomics;
+  bwd=stash   the dK/dV kernel also writes the rounded dS it computes, and a
+              dQ kernel reads it back (no recomputation, deterministic).
 
 The reference chose the split backward for determinism and named the atomic
 form as the unmeasured alternative (AttentionBackwardKernel.swift:27-41,
 docs/COMPARISON.md:151-154); its backward tests set the bar used here
 (AttentionBackwardTests.swift: hybrid error against an fp64 oracle).
 
-Checks: parity with the fp64 oracle at small and ragged shapes, dK/dV
-bit-identical to the split kernels (the same per-block arithmetic), dQ of two
-runs within one rounding unit of each other, and, at the headline causal shape
-(B4 H32 S4096 D128) in full, dK/dV identical to and dQ within the parity
-tolerance of the split path."""
+Checks, for both forms: parity with the fp64 oracle at small and ragged
+shapes, dK/dV bit-identical to the split kernels (the same per-block
+arithmetic), dQ of two runs within one rounding unit of each other (atomic) or
+identical (stash), and, at the headline causal shape (B4 H32 S4096 D128) in
+full, dK/dV identical to and dQ within the parity tolerance of the split
+path."""
 
 import math
 
@@ -32,7 +35,7 @@ B, I, F = _core.ARG_BUFFER, _core.ARG_I32, _core.ARG_F32
 class _Run:
     """Q, K, V, dO uploaded once; forward, then the split and/or fused backward."""
 
-    def __init__(self, heads, seq, dim, element, causal, seed=0, inputs=None):
+    def __init__(self, heads, seq, dim, element, causal, seed=0, inputs=None, bwd="atomic"):
         self.heads, self.seq, self.dim = heads, seq, dim
         self.element, self.causal = element, causal
         if inputs is None:
@@ -49,7 +52,8 @@ class _Run:
         self.bufs["delta"] = DeviceBuffer((heads, seq), "float32")
         self.scale = 1 / math.sqrt(dim)
         self.split = ops.library(element, dim, causal)
-        self.atomic = ops.library(element, dim, causal, bwd="atomic")
+        self.fused_lib = ops.library(element, dim, causal, bwd=bwd)
+        self.bwd = bwd
         sh, ss = seq * dim, dim
         self.tail = [_core.float_bits(self.scale), sh, ss, seq, seq]
         kern = self.split.kernels
@@ -75,11 +79,12 @@ class _Run:
         return self.grads()
 
     def run_fused(self):
-        kern = self.atomic.kernels["attn_bwd_fused"]
+        kern = self.fused_lib.kernels["attn_bwd_fused"]
         _core.launch(kern, (1, self.heads, 1), 128, [B] * 9 + [F, I, I, I, I],
                      [self.h(x) for x in ("q", "k", "v", "do", "dq", "dk", "dv", "lse", "delta")] +
                      self.tail)
-        assert "tm_attn_fused_fast_" in _core.kernel_variant(kern)
+        want = "tm_attn_fused_fast_" if self.bwd == "atomic" else "tm_attn_dkdv_stash_"
+        assert want in _core.kernel_variant(kern)
         return self.grads()
 
     def free(self):
@@ -87,12 +92,16 @@ class _Run:
             b.free()
 
 
+BWD = ["atomic", "stash"]
+
+
+@pytest.mark.parametrize("bwd", BWD)
 @pytest.mark.parametrize("element", ["bf16", "f16"])
 @pytest.mark.parametrize("dim", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("seq", [1, 3, 65, 129, 300])
-def test_fused_backward_matches_oracle(element, dim, causal, seq, device):
-    run = _Run(2, seq, dim, element, causal, seed=seq)
+def test_fused_backward_matches_oracle(bwd, element, dim, causal, seq, device):
+    run = _Run(2, seq, dim, element, causal, seed=seq, bwd=bwd)
     try:
         fused = run.run_fused()
         split = run.run_split()
@@ -108,12 +117,14 @@ def test_fused_backward_matches_oracle(element, dim, causal, seq, device):
     assert np.array_equal(fused["dv"], split["dv"])
 
 
-def test_fused_backward_workspace_regrows_and_is_cleared(device):
-    """One bwd=atomic library, three problems in a row (small, larger,
-    small): the library's dQ accumulator grows, and each launch starts it at
-    zero (a stale sum would double dQ)."""
+@pytest.mark.parametrize("bwd", BWD)
+def test_fused_backward_workspace_regrows_and_is_cleared(bwd, device):
+    """One library, three problems in a row (small, larger, small): the
+    library's workspace grows, and each launch starts from a clean state (a
+    stale atomic sum would double dQ; a stale stash would feed the previous
+    problem's dS)."""
     for seq, heads in ((100, 1), (700, 3), (100, 1)):
-        run = _Run(heads, seq, 128, "bf16", True, seed=seq + heads)
+        run = _Run(heads, seq, 128, "bf16", True, seed=seq + heads, bwd=bwd)
         try:
             fused = run.run_fused()
             again = run.run_fused()
@@ -125,10 +136,13 @@ def test_fused_backward_workspace_regrows_and_is_cleared(device):
         # the second launch sums the same partials in another order: one
         # rounding unit of the element type apart at most, not twice the value
         assert T.hybrid_error(again["dq"], fused["dq"]) <= 2 * T.U_BF16
+        if bwd == "stash":
+            assert np.array_equal(again["dq"], fused["dq"])
         assert np.array_equal(again["dk"], fused["dk"])
 
 
-def test_fused_backward_config5_full_size_against_split(device):
+@pytest.mark.parametrize("bwd", BWD)
+def test_fused_backward_config5_full_size_against_split(bwd, device):
     """B4 H32 S4096 D128, bf16, causal, at full size: dK and dV bit-identical
     to the split kernels, dQ within the parity tolerance of the split kernel's
     dQ, which the oracle-checked tests pin."""
@@ -136,7 +150,7 @@ def test_fused_backward_config5_full_size_against_split(device):
     rng = np.random.default_rng(5)
     inputs = [round_to(rng.standard_normal((heads, seq, dim), dtype=np.float32), "bf16")
               for _ in range(4)]
-    run = _Run(heads, seq, dim, "bf16", True, inputs=inputs)
+    run = _Run(heads, seq, dim, "bf16", True, inputs=inputs, bwd=bwd)
     try:
         split = run.run_split()
         fused = run.run_fused()

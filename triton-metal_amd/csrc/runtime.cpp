@@ -218,14 +218,19 @@ struct BuiltinSpec {
   Element element = Element::F32;
   int head_dim = 64;
   bool causal = false;
-  /* bwd=atomic: the library also offers attn_bwd_fused, the single-pass
-   * backward whose dQ is summed with floating-point atomics (not
-   * deterministic, so never the default) */
-  bool atomic_bwd = false;
+  /* bwd=atomic or bwd=stash: the library also offers attn_bwd_fused, a
+   * backward in one call.  atomic: one dK/dV/dQ kernel, dQ summed with
+   * floating-point atomics (not deterministic); stash: the dK/dV kernel
+   * writes the rounded dS it computes, and a dQ kernel reads it back instead
+   * of recomputing S and dP (deterministic; heads * n_ctx^2 * 2 bytes of
+   * workspace).  The reference's split (attn_bwd_dq + attn_bwd_dkdv) stays
+   * available in every library. */
+  enum class Bwd { Split, Atomic, Stash } bwd = Bwd::Split;
 
   std::string text() const {
     return format("builtin element=%s head_dim=%d causal=%d%s", element_name(element), head_dim,
-                  causal ? 1 : 0, atomic_bwd ? " bwd=atomic" : "");
+                  causal ? 1 : 0,
+                  bwd == Bwd::Atomic ? " bwd=atomic" : bwd == Bwd::Stash ? " bwd=stash" : "");
   }
 };
 
@@ -375,9 +380,11 @@ BuiltinSpec parse_spec(const char *text) {
       else if (value == "1" || value == "true") spec.causal = true;
       else throw TmError("built-in library spec: causal must be 0 or 1, got '" + value + "'");
     } else if (key == "bwd") {
-      if (value == "split") spec.atomic_bwd = false;
-      else if (value == "atomic") spec.atomic_bwd = true;
-      else throw TmError("built-in library spec: bwd must be split or atomic, got '" + value + "'");
+      if (value == "split") spec.bwd = BuiltinSpec::Bwd::Split;
+      else if (value == "atomic") spec.bwd = BuiltinSpec::Bwd::Atomic;
+      else if (value == "stash") spec.bwd = BuiltinSpec::Bwd::Stash;
+      else throw TmError("built-in library spec: bwd must be split, atomic or stash, got '" + value +
+                         "'");
     } else {
       throw TmError("built-in library spec: unknown key '" + key + "'");
     }
@@ -720,6 +727,40 @@ struct Scratch {
   size_t bytes = 0;
 };
 
+/* attn_bwd_fused under bwd=stash as two dispatches: the dK/dV kernel, which
+ * also writes dS^T into `stash`, then the dQ kernel that reads it.  Every
+ * stash element the dQ kernel reads for a stored query is written first (the
+ * causal dK/dV walk starts at its key block's first key, the dQ walk stops at
+ * its query block's last key; keys up to the next multiple of 128 are
+ * written), so nothing needs clearing; unwritten elements reach only the
+ * columns of queries past n_ctx, which are not stored. */
+void plan_stash_backward(Plan &plan, const BuiltinSpec &spec, const TmAttnDkdvArgs &kv, void *dq,
+                         void *stash, int32_t stash_keys, int32_t stash_blocks) {
+  const char *el = element_name(spec.element);
+  TmAttnFusedArgs f{};
+  f.kv = kv;
+  f.dq = dq;
+  f.stash = stash;
+  f.stash_keys = stash_keys;
+  f.stash_blocks = stash_blocks;
+  Plan kv_pass, dq_pass;
+  kv_pass.variant = format("tm_attn_dkdv_stash_%s_d%d%s", el, spec.head_dim,
+                           spec.causal ? "_causal" : "");
+  kv_pass.grid[0] = (unsigned)(cdiv(kv.n_ctx, 128) * kv.heads);
+  kv_pass.block = 256;
+  set_kernarg(kv_pass, f);
+  dq_pass.variant = format("tm_attn_dq_stash_%s_d%d%s", el, spec.head_dim,
+                           spec.causal ? "_causal" : "");
+  dq_pass.grid[0] = (unsigned)(cdiv(kv.n_ctx, 256) * kv.heads);
+  dq_pass.block = 512;
+  set_kernarg(dq_pass, f);
+  for (Plan *part : {&kv_pass, &dq_pass}) part->function = builtin_function(part->variant);
+  plan.variant = kv_pass.variant;
+  plan.function = kv_pass.function;
+  plan.block = kv_pass.block;
+  plan.sequence = {kv_pass, dq_pass};
+}
+
 Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, int64_t gx,
                   int64_t gy, int64_t gz, const Scratch *scratch = nullptr) {
   const BuiltinInfo &info = *find_builtin(k.name);
@@ -999,33 +1040,48 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
       kv.sm_scale = sm_scale;
       kv.head_dim = spec.head_dim;
       kv.heads = (int32_t)heads;
+      const bool stash = spec.bwd == BuiltinSpec::Bwd::Stash;
+      /* atomic: the fp32 dQ accumulator; stash: dS^T per head as [query
+       * blocks of 32, rounded up to whole 256-query blocks][keys rounded up
+       * to 128][32] */
       const int64_t count = heads * kv.n_ctx * (int64_t)spec.head_dim;
-      float *acc = nullptr;
+      const int64_t stash_keys = cdiv(kv.n_ctx, 128) * 128;
+      const int64_t stash_blocks = cdiv(kv.n_ctx, 256) * 8;
+      const int64_t stash_head = stash_blocks * stash_keys * 32 * 2;
+      if (stash && stash_head > INT32_MAX)
+        throw TmError(format("%s with bwd=stash keeps n_ctx^2 elements of dS per head and takes "
+                             "n_ctx up to 32640; got %d",
+                             nm, kv.n_ctx));
+      const size_t need = stash ? (size_t)(heads * stash_head) : (size_t)count * sizeof(float);
+      void *work = nullptr;
       if (scratch) {
-        const size_t need = (size_t)count * sizeof(float);
         if (need > scratch->bytes)
-          throw TmError(format("%s through tm_launch_noalloc needs a %zu-byte dQ accumulator "
-                               "(heads * n_ctx * head_dim * 4) but the static scratch holds %zu "
-                               "bytes; launch it with tm_launch",
-                               nm, need, scratch->bytes));
-        acc = (float *)scratch->ptr;
+          throw TmError(format("%s through tm_launch_noalloc needs a %zu-byte %s but the static "
+                               "scratch holds %zu bytes; launch it with tm_launch",
+                               nm, need,
+                               stash ? "dS stash (heads * n_ctx * n_ctx rounded up to 128 * 2)"
+                                     : "dQ accumulator (heads * n_ctx * head_dim * 4)",
+                               scratch->bytes));
+        work = scratch->ptr;
       } else {
         std::lock_guard<std::mutex> guard(lib.workspace_lock);
-        const size_t need = (size_t)count * sizeof(float);
         if (lib.workspace_bytes < need) {
-          /* the old accumulator may still be bound to a queued dispatch */
+          /* the old workspace may still be bound to a queued dispatch */
           if (lib.workspace) {
             finish(require_device().stream);
             hip_check(hipFree(lib.workspace), "hipFree");
             lib.workspace = nullptr;
             lib.workspace_bytes = 0;
           }
-          hip_check(hipMalloc(&lib.workspace, need), "hipMalloc (dQ accumulator)");
+          hip_check(hipMalloc(&lib.workspace, need), "hipMalloc (backward workspace)");
           lib.workspace_bytes = need;
         }
-        acc = (float *)lib.workspace;
+        work = lib.workspace;
       }
-      plan_fused_backward(plan, spec, kv, args[4].buffer->ptr, acc, count);
+      if (stash)
+        plan_stash_backward(plan, spec, kv, args[4].buffer->ptr, work, (int32_t)stash_keys,
+                            (int32_t)stash_blocks);
+      else plan_fused_backward(plan, spec, kv, args[4].buffer->ptr, (float *)work, count);
       return plan;
     }
     case Builtin::Probe: {
@@ -1351,7 +1407,7 @@ std::string kernel_info_json(const BuiltinSpec &spec) {
   out << "{\n  \"kernels\" : [\n";
   bool first = true;
   for (const BuiltinInfo &info : builtin_table()) {
-    if (info.id == Builtin::AttnFused && !spec.atomic_bwd) continue;
+    if (info.id == Builtin::AttnFused && spec.bwd == BuiltinSpec::Bwd::Split) continue;
     const Published pub = published_shape(info.id);
     if (!first) out << ",\n";
     first = false;
@@ -1496,10 +1552,10 @@ int64_t tm_load_kernel(int64_t library, const char *name) {
     if (!info)
       throw TmError(format("kernel '%s' not found in library (available: %s)", name,
                            builtin_names().c_str()));
-    if (info->id == Builtin::AttnFused && !lib->spec.atomic_bwd)
+    if (info->id == Builtin::AttnFused && lib->spec.bwd == BuiltinSpec::Bwd::Split)
       throw TmError("kernel 'attn_bwd_fused' is offered only by built-in libraries whose spec "
-                    "has bwd=atomic (its dQ is summed with floating-point atomics, so it is not "
-                    "deterministic)");
+                    "has bwd=atomic (dQ summed with floating-point atomics, not deterministic) "
+                    "or bwd=stash (dS kept in a workspace for the dQ pass)");
     k->builtin = info->id;
     /* load the kernel images now, so that launches (tm_launch_noalloc among
      * them) load no code; a failure here resurfaces at the first launch */

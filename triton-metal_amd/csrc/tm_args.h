@@ -73,13 +73,18 @@ struct TmAttnDkdvArgs {
   int32_t head_dim, heads;
 };
 
-/* attn_bwd_fused (built-in libraries with bwd=atomic; no reference kernel —
- * the variant the reference names at AttentionBackwardKernel.swift:27-41 and
- * docs/COMPARISON.md:151-154): the dK/dV kernel's arguments plus dQ and its
- * fp32 accumulator, [heads][n_ctx][head_dim] dense, zeroed before the launch. */
+/* attn_bwd_fused (built-in libraries with bwd=atomic or bwd=stash; no
+ * reference kernel — the single-pass variant the reference names at
+ * AttentionBackwardKernel.swift:27-41 and docs/COMPARISON.md:151-154): the
+ * dK/dV kernel's arguments plus, for bwd=atomic, dQ's fp32 accumulator
+ * ([heads][n_ctx][head_dim] dense, zeroed before the launch), or, for
+ * bwd=stash, dQ and the dS^T stash the dK/dV pass writes for the dQ pass. */
 struct TmAttnFusedArgs {
   TmAttnDkdvArgs kv;
-  float *dq_acc;
+  float *dq_acc;   /* bwd=atomic */
+  void *dq;        /* bwd=stash: dQ, and the dS^T stash, per head */
+  void *stash;     /* [stash_blocks query blocks of 32][stash_keys][32] */
+  int32_t stash_keys, stash_blocks;
 };
 
 /* The passes around attn_bwd_fused: clear dq_acc (count floats), then write

@@ -32,8 +32,9 @@ def cdiv(a, b):
 
 class BuiltinLibrary:
     """One built-in library spec and its kernels, loaded once.  bwd="atomic"
-    adds attn_bwd_fused, the single-pass backward with an atomically summed
-    (non-deterministic) dQ."""
+    or bwd="stash" adds attn_bwd_fused, the backward in one call: atomic sums
+    dQ with fp32 atomics (not deterministic); stash keeps the dS the dK/dV
+    pass computes for a dQ pass (deterministic, n_ctx^2 workspace per head)."""
 
     NAMES = ("matmul_kernel", "attn_fwd", "attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv",
              "sae_encode_kernel")
@@ -41,8 +42,8 @@ class BuiltinLibrary:
     def __init__(self, element="f32", head_dim=64, causal=False, bwd="split"):
         if element not in _ELEMENTS:
             raise ValueError(f"element must be one of {sorted(_ELEMENTS)}")
-        if bwd not in ("split", "atomic"):
-            raise ValueError("bwd must be 'split' or 'atomic'")
+        if bwd not in ("split", "atomic", "stash"):
+            raise ValueError("bwd must be 'split', 'atomic' or 'stash'")
         self.element = element
         self.dtype = _ELEMENTS[element]
         self.head_dim = head_dim
@@ -51,7 +52,7 @@ class BuiltinLibrary:
         self.spec = f"builtin element={element} head_dim={head_dim} causal={int(causal)} bwd={bwd}"
         self.info = {k["name"]: k for k in json.loads(_core.kernel_info(self.spec))["kernels"]}
         self.handle = _core.compile_msl(self.spec)
-        names = self.NAMES + (("attn_bwd_fused",) if bwd == "atomic" else ())
+        names = self.NAMES + (("attn_bwd_fused",) if bwd != "split" else ())
         self.kernels = {name: _core.load_kernel(self.handle, name) for name in names}
 
     def release(self):
@@ -205,8 +206,8 @@ class AttentionLayer:
 
     `heads` is batch*heads: the reference's layout [B*H, S, D] with
     stride_head = S*D and stride_seq = D (AttentionKernel.swift:25-28).
-    bwd="atomic" runs the backward as preprocess + attn_bwd_fused instead of
-    preprocess + dq + dkdv.
+    bwd="atomic" or "stash" runs the backward as preprocess + attn_bwd_fused
+    instead of preprocess + dq + dkdv.
     """
 
     #: per-(head, row) tensors: the forward's L (log2 units) and the backward's Delta
@@ -299,7 +300,7 @@ class AttentionLayer:
     def run_backward(self, synchronous=True):
         k = self.lib.kernels
         _go(k["attn_bwd_preprocess"], *self.pre_args(), synchronous=False)
-        if self.bwd == "atomic":
+        if self.bwd != "split":
             _go(k["attn_bwd_fused"], *self.fused_args(), synchronous=synchronous)
             return
         _go(k["attn_bwd_dq"], *self.dq_args(), synchronous=False)
