@@ -57,6 +57,26 @@ TM_DEV int xcd_remap(int wg, int nwg) {
   return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
 }
 
+/* Logical id -> (head, rank of the block's work, 0 = heaviest) for the
+ * causal kernels, whose blocks differ in work by up to the number of blocks
+ * per head.  Heads are walked in groups of G and, within a group, every
+ * head's heaviest block before any head's next one, so each group ends on the
+ * light blocks of all its heads instead of the last head's heavy ones
+ * starting late.  Measured at B4 H32 S4096 D128 (16 heads per XCD): G = 4
+ * runs the forward, dq and dkdv 4-5% faster than head by head (G = 1); G = 2
+ * and 8 gain less, G = 3 and 6 (not dividing an XCD's heads) and 16 nothing. */
+#ifndef TM_CAUSAL_GROUP
+#define TM_CAUSAL_GROUP 4
+#endif
+TM_DEV void causal_order(int logical, int nb, int heads, int &bh, int &rank) {
+  constexpr int G = TM_CAUSAL_GROUP;
+  const int group = logical / (G * nb);
+  const int r = logical - group * G * nb;
+  const int gsize = min(G, heads - group * G);
+  rank = r / gsize;
+  bh = group * G + (r - rank * gsize);
+}
+
 
 /* ---- LDS staging ----------------------------------------------------------
  * K and V tiles are copied HBM -> LDS by buffer_load_dwordx4 ... lds, which
@@ -301,9 +321,14 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   const int n = p.n_ctx;
   const int nqb = (n + BM - 1) / BM;
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = logical / nqb;
-  int qb = logical - bh * nqb;
-  if (CAUSAL) qb = nqb - 1 - qb;
+  int bh, qb;
+  if (CAUSAL) {
+    causal_order(logical, nqb, p.heads, bh, qb);
+    qb = nqb - 1 - qb;
+  } else {
+    bh = logical / nqb;
+    qb = logical - bh * nqb;
+  }
   const int q0 = qb * BM;
   const int qw0 = q0 + wave * QW;
   const int64_t base = (int64_t)bh * p.stride_head;
@@ -677,9 +702,14 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
   const int n = p.n_ctx;
   const int nqb = (n + BM - 1) / BM;
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = logical / nqb;
-  int qb = logical - bh * nqb;
-  if (CAUSAL) qb = nqb - 1 - qb;
+  int bh, qb;
+  if (CAUSAL) {
+    causal_order(logical, nqb, p.heads, bh, qb);
+    qb = nqb - 1 - qb;
+  } else {
+    bh = logical / nqb;
+    qb = logical - bh * nqb;
+  }
   const int q0 = qb * BM;
   const int qw0 = q0 + wave * QW;
   const int64_t base = (int64_t)bh * p.stride_head;
@@ -853,8 +883,13 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
   const int n = p.n_ctx;
   const int nkb = (n + BN - 1) / BN;
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = logical / nkb;
-  const int kb = logical - bh * nkb;
+  int bh, kb;
+  if (CAUSAL) {
+    causal_order(logical, nkb, p.heads, bh, kb);
+  } else {
+    bh = logical / nkb;
+    kb = logical - bh * nkb;
+  }
   const int k0 = kb * BN;
   const int kw0 = k0 + wave * KW;
   const int64_t base = (int64_t)bh * p.stride_head;
@@ -1226,9 +1261,14 @@ TM_DEV void attn_dq_stash(const TmAttnFusedArgs &a) {
   const int n = p.n_ctx;
   const int nqb = (n + BM - 1) / BM;
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = logical / nqb;
-  int qb = logical - bh * nqb;
-  if (CAUSAL) qb = nqb - 1 - qb;
+  int bh, qb;
+  if (CAUSAL) {
+    causal_order(logical, nqb, p.heads, bh, qb);
+    qb = nqb - 1 - qb;
+  } else {
+    bh = logical / nqb;
+    qb = logical - bh * nqb;
+  }
   const int q0 = qb * BM;
   const int qw0 = q0 + wave * QW;
   const int half = wave >> 2;           /* which 128-query half of the dS tile */
