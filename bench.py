@@ -84,7 +84,8 @@ def profile_pass(core, ops):
     """One copy of COPY_BYTES (reads and writes that many bytes of HBM), then one
     dispatch each of attn_fwd, attn_bwd_preprocess, attn_bwd_dq, attn_bwd_dkdv at
     config 5, the bwd=atomic backward (attn_bwd_fused: accumulator clear, fused
-    kernel, dQ conversion) at config 5, matmul_kernel at config 3 and sae_encode_kernel at 8192 x 2048 x 16384."""
+    kernel, dQ conversion) and the bwd=stash one (dK/dV with the dS stash, dQ
+    from it) at config 5, matmul_kernel at config 3 and sae_encode_kernel at 8192 x 2048 x 16384."""
     from triton_metal.buffer import DeviceBuffer
     lib = core.compile_msl(COPY_SOURCE)
     kernel = core.load_kernel(lib, "tm_calibration_copy")
@@ -101,12 +102,13 @@ def profile_pass(core, ops):
     layer.run_forward()
     layer.run_backward()
     layer.free()
-    fused = ops.AttentionLayer(B * H, S, D, "bf16", True, bwd="atomic")
-    for i, name in enumerate(("q", "k", "v", "do")):
-        fused.buffers[name].write(normal_bf16((B * H, S, D), 100 + i))
-    fused.run_forward()
-    fused.run_backward()
-    fused.free()
+    for mode in ("atomic", "stash"):
+        fused = ops.AttentionLayer(B * H, S, D, "bf16", True, bwd=mode)
+        for i, name in enumerate(("q", "k", "v", "do")):
+            fused.buffers[name].write(normal_bf16((B * H, S, D), 100 + i))
+        fused.run_forward()
+        fused.run_backward()
+        fused.free()
     n = 8192
     a = DeviceBuffer((n, n), "bfloat16").write(normal_bf16((n, n), 1))
     b = DeviceBuffer((n, n), "bfloat16").write(normal_bf16((n, n), 2))
