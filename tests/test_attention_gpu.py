@@ -48,6 +48,30 @@ def test_forward_f32_across_shapes(device, heads, seq, dim, causal):
     assert T.hybrid_error(lse, want_l) <= 2e-5
 
 
+@pytest.mark.parametrize("stats", [True, False])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("heads,seq,dim", [(1, 512, 64), (2, 300, 96), (1, 1000, 32), (3, 129, 128)])
+def test_forward_f32_key_range_split(device, heads, seq, dim, causal, stats):
+    """Grids too small to fill the chip split each workgroup's key blocks into
+    ranges whose partials a second dispatch combines; same answers at 2e-5,
+    including causal rows whose later ranges hold no visible key, and the
+    8-argument form that writes no L."""
+    q, k, v, _ = inputs(heads, seq, dim)
+    r = Runner(heads, seq, dim, "f32", causal)
+    try:
+        r.layer.buffers["lse"].write(np.full((heads, seq), 7.0, np.float32))
+        o, lse = r.forward(q, k, v, stats=stats)
+    finally:
+        r.free()
+    assert "key ranges" in r.variant, r.variant
+    want_o, _, want_l = R.attention_forward(q, k, v, r.scale, causal)
+    assert T.hybrid_error(o, want_o) <= 2e-5
+    if stats:
+        assert T.hybrid_error(lse, want_l) <= 2e-5
+    else:
+        assert np.all(lse == 7.0)
+
+
 @pytest.mark.parametrize("element,tol", [("f16", 4e-3), ("bf16", 2e-2)])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("heads,seq,dim", [(2, 127, 64), (1, 128, 64), (2, 200, 128),
@@ -128,6 +152,34 @@ def test_gradients_match_the_analytic_reference(device, heads, seq, dim, element
     _assert_within_bound(dq, want["dq"], terms, u, amp["dq"], "dQ")
     _assert_within_bound(dk, want["dk"], terms, u, amp["dk"], "dK")
     _assert_within_bound(dv, want["dv"], terms, u, amp["dv"], "dV")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("heads,seq,dim,element", [(1, 512, 64, "f32"), (2, 300, 96, "f32"),
+                                                   (1, 1000, 32, "f32"), (3, 129, 128, "f32"),
+                                                   (1, 300, 80, "bf16")])
+def test_gradients_key_and_query_range_split(device, heads, seq, dim, element, causal):
+    """Grids too small to fill the chip split dq's key blocks and dkdv's query
+    blocks into ranges whose fp32 partials a second dispatch sums (with
+    sm_scale and the output rounding): the same bound as the unsplit kernels,
+    including causal ranges that hold no visible pair."""
+    q, k, v, d_out = inputs(heads, seq, dim, element)
+    r = Runner(heads, seq, dim, element, causal)
+    want = oracle(q, k, v, d_out, r.scale, causal)
+    try:
+        delta, dq, dk, dv = r.backward(q, k, v, want["o"], want["lse"], d_out)
+    finally:
+        r.free()
+    assert all("ranges" in v for v in r.variants[1:]), r.variants
+    amp = want["amplification"]
+    if element == "f32":
+        terms = seq + dim + 2
+        _assert_within_bound(dq, want["dq"], terms, T.U_F32, amp["dq"], "dQ")
+        _assert_within_bound(dk, want["dk"], terms, T.U_F32, amp["dk"], "dK")
+        _assert_within_bound(dv, want["dv"], terms, T.U_F32, amp["dv"], "dV")
+    else:
+        for name, got in (("dq", dq), ("dk", dk), ("dv", dv)):
+            assert T.hybrid_error(got, want[name]) <= 2e-2, name
 
 
 @pytest.mark.parametrize("causal", [False, True])

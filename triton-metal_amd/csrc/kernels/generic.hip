@@ -174,10 +174,16 @@ TM_DEV void attn_fwd_generic(const TmAttnFwdArgs &p) {
 #pragma unroll
   for (int i = 0; i < DP / 16; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  const int kend = CAUSAL ? min(n, q0 + BM) : n;
+  /* the key blocks this workgroup walks: all of them, or the split-th of
+   * `splits` contiguous ranges */
+  const int kend_all = CAUSAL ? min(n, q0 + BM) : n;
+  const int nkb = (kend_all + BN - 1) / BN;
+  const int split = blockIdx.z;
+  const int kbeg = p.splits > 1 ? (int)((int64_t)split * nkb / p.splits) * BN : 0;
+  const int kend = p.splits > 1 ? min(kend_all, (int)((int64_t)(split + 1) * nkb / p.splits) * BN) : kend_all;
   TileStager<T, BN, DP> kv;
-  if (kend > 0) kv.load(K, V, 0, n, D, p.stride_seq, tid);
-  for (int k0 = 0; k0 < kend; k0 += BN) {
+  if (kbeg < kend) kv.load(K, V, kbeg, n, D, p.stride_seq, tid);
+  for (int k0 = kbeg; k0 < kend; k0 += BN) {
     __syncthreads();
     kv.store(Ks, Vs, tid);
     __syncthreads();
@@ -202,16 +208,20 @@ TM_DEV void attn_fwd_generic(const TmAttnFwdArgs &p) {
     }
     mx = group4_max(mx);
     const float m_new = fmaxf(m_i, mx);
+    /* a row whose keys so far are all masked (the first blocks of a key
+     * range above a causal query) keeps P = 0 and l = 0 instead of
+     * exp2(-inf - -inf) */
+    const float m_use = m_new == TM_NEG_INF ? 0.f : m_new;
     float rs = 0.f;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sc[t][r] = exp2f(sc[t][r] - m_new);
+        sc[t][r] = exp2f(sc[t][r] - m_use);
         rs += sc[t][r];
       }
     rs = group4_sum(rs);
-    const float alpha = exp2f(m_i - m_new);
+    const float alpha = exp2f(m_i - m_use);
     l_i = l_i * alpha + rs;
     m_i = m_new;
 #pragma unroll
@@ -226,7 +236,23 @@ TM_DEV void attn_fwd_generic(const TmAttnFwdArgs &p) {
     }
   }
 
-  if (qi < n) {
+  if (qi < n && p.splits > 1) {
+    /* partials of this key range: unnormalised O, then (m, l) */
+    float *po = p.part + (((int64_t)split * p.heads + bh) * n + qi) * D;
+#pragma unroll
+    for (int dt = 0; dt < DP / 16; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = dt * 16 + 4 * g + r;
+        if (d < D) po[d] = acc[dt][r];
+      }
+    if (g == 0) {
+      float *pml = p.part + (int64_t)p.splits * p.heads * n * D +
+                   (((int64_t)split * p.heads + bh) * n + qi) * 2;
+      pml[0] = m_i;
+      pml[1] = l_i;
+    }
+  } else if (qi < n) {
     const float inv = 1.f / l_i;
 #pragma unroll
     for (int dt = 0; dt < DP / 16; ++dt)
@@ -237,6 +263,57 @@ TM_DEV void attn_fwd_generic(const TmAttnFwdArgs &p) {
       }
     if (p.lse && g == 0) p.lse[(int64_t)bh * p.stride_lse + qi] = m_i + log2f(l_i);
   }
+}
+
+/* The forward's key-range partials combined (TmAttnFwdArgs.part): for each
+ * row, m = max_s m_s, l = sum_s 2^(m_s - m) l_s, O = sum_s 2^(m_s - m) O_s / l,
+ * L = m + log2(l) -- the online softmax's own rescaling, applied across the
+ * ranges.  Ranges with l_s = 0 (every key masked for the row) add nothing.
+ * 64 threads per row (head_dim up to 128), 4 rows per workgroup. */
+template <typename T>
+TM_DEV void attn_fwd_combine(const TmAttnFwdArgs &p) {
+  constexpr int SMAX = 16; /* the planner's largest split */
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n = p.n_ctx, D = p.head_dim, S = p.splits;
+  if (row >= (int64_t)p.heads * n) return;
+  const int bh = (int)(row / n), q = (int)(row - (int64_t)bh * n);
+  const int lane = threadIdx.x & 63;
+  const int64_t range = (int64_t)p.heads * n; /* rows per range */
+  const float *pml = p.part + (int64_t)S * range * D;
+  /* every range's (m, l), then every range's two O values, each as one batch
+   * of independent loads */
+  float m_s[SMAX], l_s[SMAX];
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) {
+    const bool in = s < S;
+    m_s[s] = in ? pml[(s * range + row) * 2] : 0.f;
+    l_s[s] = in ? pml[(s * range + row) * 2 + 1] : 0.f;
+  }
+  float o0_s[SMAX], o1_s[SMAX];
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) {
+    const float *po = p.part + (s * range + row) * D;
+    o0_s[s] = s < S && lane < D ? po[lane] : 0.f;
+    o1_s[s] = s < S && lane + 64 < D ? po[lane + 64] : 0.f;
+  }
+  float m = TM_NEG_INF;
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s)
+    if (l_s[s] > 0.f) m = fmaxf(m, m_s[s]);
+  float l = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) {
+    if (!(l_s[s] > 0.f)) continue;
+    const float w = exp2f(m_s[s] - m);
+    l += w * l_s[s];
+    o0 += w * o0_s[s];
+    o1 += w * o1_s[s];
+  }
+  const float inv = 1.f / l;
+  T *O = (T *)p.o + (int64_t)bh * p.stride_head + (int64_t)q * p.stride_seq;
+  if (lane < D) O[lane] = from_f32<T>(o0 * inv);
+  if (lane + 64 < D) O[lane + 64] = from_f32<T>(o1 * inv);
+  if (p.lse && lane == 0) p.lse[(int64_t)bh * p.stride_lse + q] = m + log2f(l);
 }
 
 /* ---------------------------------------------------------------------------
@@ -305,10 +382,14 @@ TM_DEV void attn_dq_generic(const TmAttnDqArgs &p) {
 #pragma unroll
   for (int i = 0; i < DP / 16; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  const int kend = CAUSAL ? min(n, q0 + BM) : n;
+  const int kend_all = CAUSAL ? min(n, q0 + BM) : n;
+  const int nkb = (kend_all + BN - 1) / BN;
+  const int split = blockIdx.z;
+  const int kbeg = p.splits > 1 ? (int)((int64_t)split * nkb / p.splits) * BN : 0;
+  const int kend = p.splits > 1 ? min(kend_all, (int)((int64_t)(split + 1) * nkb / p.splits) * BN) : kend_all;
   TileStager<T, BN, DP> kv;
-  if (kend > 0) kv.load(K, V, 0, n, D, p.stride_seq, tid);
-  for (int k0 = 0; k0 < kend; k0 += BN) {
+  if (kbeg < kend) kv.load(K, V, kbeg, n, D, p.stride_seq, tid);
+  for (int k0 = kbeg; k0 < kend; k0 += BN) {
     __syncthreads();
     kv.store(Ks, Vs, tid);
     __syncthreads();
@@ -343,12 +424,15 @@ TM_DEV void attn_dq_generic(const TmAttnDqArgs &p) {
   }
 
   if (qi < n) {
+    float *po = p.splits > 1 ? p.part + (((int64_t)split * p.heads + bh) * n + qi) * D : nullptr;
 #pragma unroll
     for (int dt = 0; dt < DP / 16; ++dt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int d = dt * 16 + 4 * g + r;
-        if (d < D) dQ[(int64_t)qi * p.stride_seq + d] = from_f32<T>(acc[dt][r] * p.sm_scale);
+        if (d >= D) continue;
+        if (po) po[d] = acc[dt][r];
+        else dQ[(int64_t)qi * p.stride_seq + d] = from_f32<T>(acc[dt][r] * p.sm_scale);
       }
   }
 }
@@ -399,7 +483,11 @@ TM_DEV void attn_dkdv_generic(const TmAttnDkdvArgs &p) {
     dv[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
   }
 
-  const int qstart = CAUSAL ? (k0 / BM) * BM : 0;
+  const int qfirst = CAUSAL ? (k0 / BM) * BM : 0;
+  const int nqb = (n - qfirst + BM - 1) / BM;
+  const int split = blockIdx.z;
+  const int qstart = p.splits > 1 ? qfirst + (int)((int64_t)split * nqb / p.splits) * BM : qfirst;
+  const int qstop = p.splits > 1 ? min(n, qfirst + (int)((int64_t)(split + 1) * nqb / p.splits) * BM) : n;
   TileStager<T, BM, DP> qdo;
   float l_next = 0.f, d_next = 0.f; /* thread tid < BM: L and Delta of row tid */
   auto load_stats = [&](int q0) {
@@ -407,11 +495,11 @@ TM_DEV void attn_dkdv_generic(const TmAttnDkdvArgs &p) {
     l_next = tid < BM && qi < n ? Lrow[qi] : 0.f;
     d_next = tid < BM && qi < n ? Drow[qi] : 0.f;
   };
-  if (qstart < n) {
+  if (qstart < qstop) {
     qdo.load(Q, dO, qstart, n, D, p.stride_seq, tid);
     load_stats(qstart);
   }
-  for (int q0 = qstart; q0 < n; q0 += BM) {
+  for (int q0 = qstart; q0 < qstop; q0 += BM) {
     __syncthreads();
     qdo.store(Qs, dOs, tid);
     if (tid < BM) {
@@ -419,7 +507,7 @@ TM_DEV void attn_dkdv_generic(const TmAttnDkdvArgs &p) {
       Ds[tid] = d_next;
     }
     __syncthreads();
-    if (q0 + BM < n) {
+    if (q0 + BM < qstop) {
       qdo.load(Q, dO, q0 + BM, n, D, p.stride_seq, tid);
       load_stats(q0 + BM);
     }
@@ -457,17 +545,56 @@ TM_DEV void attn_dkdv_generic(const TmAttnDkdvArgs &p) {
   }
 
   if (kj < n) {
+    const int64_t plane = (int64_t)p.heads * n * D;
+    float *pk = p.splits > 1 ? p.part + 2 * split * plane + ((int64_t)bh * n + kj) * D : nullptr;
 #pragma unroll
     for (int dt = 0; dt < DP / 16; ++dt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int d = dt * 16 + 4 * g + r;
-        if (d < D) {
+        if (d >= D) continue;
+        if (pk) {
+          pk[d] = dk[dt][r];
+          pk[plane + d] = dv[dt][r];
+        } else {
           const int64_t off = (int64_t)kj * p.stride_seq + d;
           dK[off] = from_f32<T>(dk[dt][r] * p.sm_scale);
           dV[off] = from_f32<T>(dv[dt][r]);
         }
       }
+  }
+}
+
+/* The backward's range partials summed (TmAttnSplitReduceArgs): one row of
+ * each output per 64 lanes (head_dim up to 128), 4 rows per workgroup, every
+ * range's values loaded as one batch. */
+template <typename T>
+TM_DEV void attn_split_reduce(const TmAttnSplitReduceArgs &p) {
+  constexpr int SMAX = 16; /* the planner's largest split */
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n = p.n_ctx, D = p.head_dim, S = p.splits;
+  if (row >= (int64_t)p.heads * n) return;
+  const int bh = (int)(row / n), q = (int)(row - (int64_t)bh * n);
+  const int lane = threadIdx.x & 63;
+  const int64_t plane = (int64_t)p.heads * n * D;
+  for (int w = 0; w < p.outputs; ++w) {
+    float v0[SMAX], v1[SMAX];
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      const float *src = p.part + (int64_t)(s * p.outputs + w) * plane + row * D;
+      v0[s] = s < S && lane < D ? src[lane] : 0.f;
+      v1[s] = s < S && lane + 64 < D ? src[lane + 64] : 0.f;
+    }
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      a0 += v0[s];
+      a1 += v1[s];
+    }
+    const float scale = w ? p.scale1 : p.scale0;
+    T *out = (T *)(w ? p.out1 : p.out0) + (int64_t)bh * p.stride_head + (int64_t)q * p.stride_seq;
+    if (lane < D) out[lane] = from_f32<T>(a0 * scale);
+    if (lane + 64 < D) out[lane + 64] = from_f32<T>(a1 * scale);
   }
 }
 
@@ -499,6 +626,23 @@ extern "C" __global__ __launch_bounds__(64) void tm_probe(float *out) {
 TM_GEMM(float, tm_gemm_generic_f32, tm_sae_generic_f32)
 TM_GEMM(f16_t, tm_gemm_generic_f16, tm_sae_generic_f16)
 TM_GEMM(bf16_t, tm_gemm_generic_bf16, tm_sae_generic_bf16)
+
+#define TM_FWD_COMBINE(T, TN)                                                                  \
+  extern "C" __global__ __launch_bounds__(256) void tm_attn_fwd_combine_##TN(TmAttnFwdArgs p) {  \
+    attn_fwd_combine<T>(p);                                                                    \
+  }
+TM_FWD_COMBINE(float, f32)
+TM_FWD_COMBINE(f16_t, f16)
+TM_FWD_COMBINE(bf16_t, bf16)
+
+#define TM_SPLIT_REDUCE(T, TN)                                                                  \
+  extern "C" __global__ __launch_bounds__(256) void tm_attn_split_reduce_##TN(                   \
+      TmAttnSplitReduceArgs p) {                                                                \
+    attn_split_reduce<T>(p);                                                                    \
+  }
+TM_SPLIT_REDUCE(float, f32)
+TM_SPLIT_REDUCE(f16_t, f16)
+TM_SPLIT_REDUCE(bf16_t, bf16)
 
 #define TM_PRE(T, NAME) \
   extern "C" __global__ __launch_bounds__(256) void NAME(TmAttnPreArgs p) { attn_pre_generic<T>(p); }

@@ -727,6 +727,27 @@ struct Scratch {
   size_t bytes = 0;
 };
 
+/* `need` bytes of device work memory for one planned dispatch sequence: the
+ * static scratch under tm_launch_noalloc (nullptr when it is too small), else
+ * the library's workspace, grown on demand.  Dispatches of one library run in
+ * order on its stream, so consecutive sequences may share the workspace. */
+void *plan_workspace(const Library &lib, size_t need, const Scratch *scratch) {
+  if (scratch) return need <= scratch->bytes ? scratch->ptr : nullptr;
+  std::lock_guard<std::mutex> guard(lib.workspace_lock);
+  if (lib.workspace_bytes < need) {
+    /* the old workspace may still be bound to a queued dispatch */
+    if (lib.workspace) {
+      finish(require_device().stream);
+      hip_check(hipFree(lib.workspace), "hipFree");
+      lib.workspace = nullptr;
+      lib.workspace_bytes = 0;
+    }
+    hip_check(hipMalloc(&lib.workspace, need), "hipMalloc (workspace)");
+    lib.workspace_bytes = need;
+  }
+  return lib.workspace;
+}
+
 /* attn_bwd_fused under bwd=stash as two dispatches: the dK/dV kernel, which
  * also writes dS^T into `stash`, then the dQ kernel that reads it.  Every
  * stash element the dQ kernel reads for a stored query is written first (the
@@ -759,6 +780,51 @@ void plan_stash_backward(Plan &plan, const BuiltinSpec &spec, const TmAttnDkdvAr
   plan.function = kv_pass.function;
   plan.block = kv_pass.block;
   plan.sequence = {kv_pass, dq_pass};
+}
+
+/* Ranges to split a generic attention kernel's walk into when its grid of
+ * `wgs` 64-row workgroups cannot fill the chip twice: enough to (at most 16,
+ * each at least two 32-row blocks of the `n_ctx` walked); 1 for no split. */
+int64_t split_ranges(int64_t wgs, int64_t n_ctx) {
+  const int64_t cus = std::max(device().compute_units, 1);
+  if (wgs >= 2 * cus) return 1;
+  return std::max<int64_t>(1, std::min<int64_t>({cdiv(2 * cus, wgs), cdiv(n_ctx, 32) / 2, 16}));
+}
+
+/* The split form of a generic dq or dkdv plan: the main dispatch over
+ * `splits` ranges (grid z) writing fp32 partials to `part`, then the reduce
+ * dispatch that sums them into the outputs (dQ * sm_scale, or dK * sm_scale
+ * and dV) in the element type. */
+template <typename A>
+void plan_split_backward(Plan &plan, const BuiltinSpec &spec, A p, float *part, int64_t splits,
+                         void *out0, void *out1) {
+  p.part = part;
+  p.splits = (int32_t)splits;
+  Plan main = plan, reduce;
+  main.grid[2] = (unsigned)splits;
+  set_kernarg(main, p);
+  TmAttnSplitReduceArgs r{};
+  r.part = part;
+  r.out0 = out0;
+  r.out1 = out1;
+  r.scale0 = p.sm_scale;
+  r.scale1 = 1.f;
+  r.stride_head = p.stride_head;
+  r.stride_seq = p.stride_seq;
+  r.n_ctx = p.n_ctx;
+  r.head_dim = p.head_dim;
+  r.heads = p.heads;
+  r.splits = (int32_t)splits;
+  r.outputs = out1 ? 2 : 1;
+  reduce.variant = format("tm_attn_split_reduce_%s", element_name(spec.element));
+  reduce.grid[0] = (unsigned)cdiv((int64_t)p.heads * p.n_ctx, 4);
+  reduce.block = 256;
+  set_kernarg(reduce, r);
+  for (Plan *part_plan : {&main, &reduce}) part_plan->function = builtin_function(part_plan->variant);
+  plan.function = main.function;
+  plan.variant = format("%s + %s (%d ranges)", main.variant.c_str(), reduce.variant.c_str(),
+                        (int)splits);
+  plan.sequence = {main, reduce};
 }
 
 Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, int64_t gx,
@@ -883,6 +949,32 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         plan.grid[0] = (unsigned)cdiv(p.n_ctx, 64);
         plan.grid[1] = (unsigned)heads;
         plan.block = 256;
+        /* Too few 64-query workgroups to fill the chip twice, each walking
+         * many key blocks: split every workgroup's key blocks into `splits`
+         * ranges (at least two 32-key blocks each) and combine the ranges'
+         * partials in a second dispatch. */
+        const int64_t splits = split_ranges((int64_t)plan.grid[0] * heads, p.n_ctx);
+        if (splits > 1) {
+          const size_t need =
+              (size_t)splits * (size_t)heads * (size_t)p.n_ctx * (size_t)(spec.head_dim + 2) * 4;
+          if (void *work = plan_workspace(lib, need, scratch)) {
+            p.part = (float *)work;
+            p.splits = (int32_t)splits;
+            Plan main = plan, combine;
+            main.grid[2] = (unsigned)splits;
+            set_kernarg(main, p);
+            combine.variant = format("tm_attn_fwd_combine_%s", el);
+            combine.grid[0] = (unsigned)cdiv(heads * p.n_ctx, 4);
+            combine.block = 256;
+            set_kernarg(combine, p);
+            for (Plan *part : {&main, &combine}) part->function = builtin_function(part->variant);
+            plan.function = main.function;
+            plan.variant = format("%s + %s (%d key ranges)", main.variant.c_str(),
+                                  combine.variant.c_str(), (int)splits);
+            plan.sequence = {main, combine};
+            return plan;
+          }
+        }
       }
       set_kernarg(plan, p);
       break;
@@ -978,6 +1070,15 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         p.head_dim = spec.head_dim;
         p.heads = (int32_t)heads;
         plan.variant = fast ? fast_name : attn_symbol("dq", spec);
+        const int64_t splits = fast ? 1 : split_ranges((int64_t)plan.grid[0] * heads, n_ctx);
+        void *work = splits > 1 ? plan_workspace(lib, (size_t)splits * (size_t)heads * (size_t)n_ctx *
+                                                          (size_t)spec.head_dim * 4,
+                                                 scratch)
+                                : nullptr;
+        if (work) {
+          plan_split_backward(plan, spec, p, (float *)work, splits, p.dq, nullptr);
+          return plan;
+        }
         set_kernarg(plan, p);
       } else {
         TmAttnDkdvArgs p{};
@@ -997,6 +1098,15 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         p.head_dim = spec.head_dim;
         p.heads = (int32_t)heads;
         plan.variant = fast ? fast_name : attn_symbol("dkdv", spec);
+        const int64_t splits = fast ? 1 : split_ranges((int64_t)plan.grid[0] * heads, n_ctx);
+        void *work = splits > 1 ? plan_workspace(lib, (size_t)splits * 2 * (size_t)heads *
+                                                          (size_t)n_ctx * (size_t)spec.head_dim * 4,
+                                                 scratch)
+                                : nullptr;
+        if (work) {
+          plan_split_backward(plan, spec, p, (float *)work, splits, p.dk, p.dv);
+          return plan;
+        }
         set_kernarg(plan, p);
       }
       break;
@@ -1053,31 +1163,14 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
                              "n_ctx up to 32640; got %d",
                              nm, kv.n_ctx));
       const size_t need = stash ? (size_t)(heads * stash_head) : (size_t)count * sizeof(float);
-      void *work = nullptr;
-      if (scratch) {
-        if (need > scratch->bytes)
-          throw TmError(format("%s through tm_launch_noalloc needs a %zu-byte %s but the static "
-                               "scratch holds %zu bytes; launch it with tm_launch",
-                               nm, need,
-                               stash ? "dS stash (heads * n_ctx * n_ctx rounded up to 128 * 2)"
-                                     : "dQ accumulator (heads * n_ctx * head_dim * 4)",
-                               scratch->bytes));
-        work = scratch->ptr;
-      } else {
-        std::lock_guard<std::mutex> guard(lib.workspace_lock);
-        if (lib.workspace_bytes < need) {
-          /* the old workspace may still be bound to a queued dispatch */
-          if (lib.workspace) {
-            finish(require_device().stream);
-            hip_check(hipFree(lib.workspace), "hipFree");
-            lib.workspace = nullptr;
-            lib.workspace_bytes = 0;
-          }
-          hip_check(hipMalloc(&lib.workspace, need), "hipMalloc (backward workspace)");
-          lib.workspace_bytes = need;
-        }
-        work = lib.workspace;
-      }
+      void *work = plan_workspace(lib, need, scratch);
+      if (!work)
+        throw TmError(format("%s through tm_launch_noalloc needs a %zu-byte %s but the static "
+                             "scratch holds %zu bytes; launch it with tm_launch",
+                             nm, need,
+                             stash ? "dS stash (heads * n_ctx * n_ctx rounded up to 128 * 2)"
+                                   : "dQ accumulator (heads * n_ctx * head_dim * 4)",
+                             scratch->bytes));
       if (stash)
         plan_stash_backward(plan, spec, kv, args[4].buffer->ptr, work, (int32_t)stash_keys,
                             (int32_t)stash_blocks);

@@ -36,6 +36,23 @@ struct TmAttnFwdArgs {
   float sm_scale;
   int32_t stride_head, stride_seq, n_ctx, stride_lse;
   int32_t head_dim, heads;
+  /* key-range split (small grids): with splits > 1, workgroup z takes the
+   * z-th of `splits` ranges of its key blocks and writes fp32 partials to
+   * `part` -- [splits][heads][n_ctx][head_dim] unnormalised O, then
+   * [splits][heads][n_ctx][2] (row offset m, row sum l) -- which
+   * tm_attn_fwd_combine_* turns into O and L */
+  float *part;
+  int32_t splits;
+};
+
+/* out_w[bh, q, :] = scale_w * sum_s part[s][w][bh][q][:] in the element type
+ * at the caller's strides, w < outputs (the split dQ, or dK and dV) */
+struct TmAttnSplitReduceArgs {
+  const float *part;
+  void *out0;
+  void *out1;
+  float scale0, scale1;
+  int32_t stride_head, stride_seq, n_ctx, head_dim, heads, splits, outputs;
 };
 
 struct TmAttnPreArgs {
@@ -57,6 +74,11 @@ struct TmAttnDqArgs {
   float sm_scale;
   int32_t stride_head, stride_seq, stride_lse, n_ctx;
   int32_t head_dim, heads;
+  /* key-range split (small grids, generic kernels): workgroup z walks the
+   * z-th of `splits` ranges of its key blocks and writes its unscaled fp32 dQ
+   * to part [splits][heads][n_ctx][head_dim], summed by tm_attn_split_reduce_* */
+  float *part;
+  int32_t splits;
 };
 
 struct TmAttnDkdvArgs {
@@ -71,6 +93,11 @@ struct TmAttnDkdvArgs {
   float sm_scale;
   int32_t stride_head, stride_seq, stride_lse, n_ctx;
   int32_t head_dim, heads;
+  /* query-range split (small grids, generic kernels): workgroup z walks the
+   * z-th of `splits` ranges of its query blocks and writes its unscaled fp32
+   * dK then dV to part [splits][2][heads][n_ctx][head_dim] */
+  float *part;
+  int32_t splits;
 };
 
 /* attn_bwd_fused (built-in libraries with bwd=atomic or bwd=stash; no
