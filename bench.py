@@ -536,12 +536,15 @@ def main():
             ms, variant = bench_gemm(core, ops, n, 2, args.sample_ms, element="f32")
             ref[f"gemm_f32_{n}"] = {"tflops": round(gemm_flops(n, n, n) / (ms * 1e-3) / 1e12, 2),
                                     "ms": round(ms, 4), "variant": variant}
-        for heads, seq in ((8, 512), (8, 1024), (16, 2048)):
+        # fp32 at three shapes, f16 at the two the reference also publishes in f16
+        # (docs/ARCHITECTURE.md:1187-1188, :1265-1266)
+        for element, heads, seq in (("f32", 8, 512), ("f32", 8, 1024), ("f32", 16, 2048),
+                                    ("f16", 8, 512), ("f16", 8, 1024)):
             _, kr = bench_attention(core, ops, 1, heads, seq, 64, False, 0, 2, args.sample_ms,
-                                    element="f32")
+                                    element=element)
             ms_f = kr["attn_fwd"]["ms"]
             ms_b = sum(kr[k]["ms"] for k in ("attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv"))
-            ref[f"fa2_f32_h{heads}_s{seq}_d64"] = {
+            ref[f"fa2_{element}_h{heads}_s{seq}_d64"] = {
                 "fwd_tflops": round(attention_flops(heads, seq, 64, False) / (ms_f * 1e-3) / 1e12, 3),
                 "bwd_tflops": round(attention_flops(heads, seq, 64, False, backward=True)
                                     / (ms_b * 1e-3) / 1e12, 3),
