@@ -318,7 +318,9 @@ TM_DEV void attn_fwd_combine(const TmAttnFwdArgs &p) {
 
 /* ---------------------------------------------------------------------------
  * attn_bwd_preprocess: Delta_i = sum_d dO_id * O_id in f32
- * (AttentionBackwardKernel.swift:53-136).  64 rows per workgroup.
+ * (AttentionBackwardKernel.swift:53-136).  64 rows per workgroup, 16 per
+ * wave: 16 lanes share a row (lane l sums d = l % 16 + 16 j), four rows at a
+ * time with all their loads issued together, then a 16-lane reduction.
  * ------------------------------------------------------------------------- */
 template <typename T>
 TM_DEV void attn_pre_generic(const TmAttnPreArgs &p) {
@@ -327,16 +329,24 @@ TM_DEV void attn_pre_generic(const TmAttnPreArgs &p) {
   const int64_t base = (int64_t)bh * p.stride_head;
   const T *O = (const T *)p.o + base;
   const T *dO = (const T *)p.dout + base;
-  for (int rr = 0; rr < 16; ++rr) {
-    const int row = blockIdx.x * 64 + wave * 16 + rr;
-    if (row >= p.n_ctx) break;
+  const int sub = lane & 15, grp = lane >> 4;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int row = blockIdx.x * 64 + wave * 16 + it * 4 + grp;
     float acc = 0.f;
-    for (int d = lane; d < p.head_dim; d += 64) {
-      const int64_t off = (int64_t)row * p.stride_seq + d;
-      acc += to_f32(O[off]) * to_f32(dO[off]);
+    if (row < p.n_ctx) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { /* head_dim <= 128 */
+        const int d = sub + 16 * j;
+        if (d < p.head_dim) {
+          const int64_t off = (int64_t)row * p.stride_seq + d;
+          acc += to_f32(O[off]) * to_f32(dO[off]);
+        }
+      }
     }
-    acc = wave_sum(acc);
-    if (lane == 0) p.delta[(int64_t)bh * p.stride_lse + row] = acc;
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (sub == 0 && row < p.n_ctx) p.delta[(int64_t)bh * p.stride_lse + row] = acc;
   }
 }
 
