@@ -3,7 +3,8 @@ their work buffer (attn_bwd_fused's fp32 dQ accumulator) from a static device
 array instead of library-owned memory.  Checked against tm_launch on the same
 inputs, two calls in a row with the second smaller (the array keeps the first
 call's contents, so a missing clear would show), a request larger than the
-array refused before anything runs, and a built-in with no work buffer."""
+array refused before anything runs, a built-in with no work buffer, and the
+generic kernels' range split, whose partials also come from the array."""
 
 import ctypes
 import math
@@ -129,3 +130,40 @@ def test_noalloc_runs_kernels_without_a_work_buffer(device):
     finally:
         for x in (a, b, c1, c2):
             x.free()
+
+
+def test_noalloc_range_split_matches_tm_launch_twice(device):
+    """The generic kernels' range split (small fp32 grids) takes its partials
+    from the static array too: forward, dq and dkdv through either entry
+    point, two problems in a row with the second smaller, give the same
+    answers bit for bit (the same dispatches over the same inputs)."""
+    for heads, seq, dim in ((2, 700, 64), (1, 300, 32)):
+        print(f"noalloc range split heads={heads} seq={seq} dim={dim}", flush=True)
+        rng = np.random.default_rng(seq)
+        layer = ops.AttentionLayer(heads, seq, dim, "f32", causal=True)
+        try:
+            for name in ("q", "k", "v", "do"):
+                layer.upload(name, rng.standard_normal((heads, seq, dim), dtype=np.float32))
+            kern = layer.lib.kernels
+            results = {}
+            for entry in ("tm_launch", "tm_launch_noalloc"):
+                out = {}
+                for name, (grid, kinds, values), reads in (
+                        ("attn_fwd", layer.fwd_args(True), ("o", "lse")),
+                        ("attn_bwd_preprocess", layer.pre_args(), ("delta",)),
+                        ("attn_bwd_dq", layer.dq_args(), ("dq",)),
+                        ("attn_bwd_dkdv", layer.dkdv_args(), ("dk", "dv"))):
+                    for r in reads:
+                        layer.buffers[r].write(np.full(layer.buffers[r].shape, 5.0, np.float32))
+                    assert _raw_launch(entry, kern[name], grid, kinds, values) == 0, _core.last_error()
+                    if name != "attn_bwd_preprocess":
+                        assert "ranges" in _core.kernel_variant(kern[name]), _core.kernel_variant(kern[name])
+                    out.update({r: layer.read(r) for r in reads})
+                results[entry] = out
+            for r, want in results["tm_launch"].items():
+                assert np.array_equal(results["tm_launch_noalloc"][r], want), r
+            q, k, v, d_out = (layer.read(x) for x in ("q", "k", "v", "do"))
+            want_o, _, _ = R.attention_forward(q, k, v, layer.scale, True)
+            assert T.hybrid_error(results["tm_launch_noalloc"]["o"], want_o) <= 2e-5
+        finally:
+            layer.free()
