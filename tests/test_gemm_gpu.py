@@ -141,17 +141,18 @@ def test_config1_fp32_256_uniform(device):
     a = G.uniform((256, 256), seed=0)
     b = G.uniform((256, 256), seed=1)
     c, variant = run_matmul(a.reshape(-1), b.reshape(-1), 256, 256, 256, (256, 1, 256, 1, 256, 1))
-    assert variant == "tm_gemm_fast_t64_f32"  # 16 tiles of 64 x 64
+    assert variant == "tm_gemm_fast_t64_k4_f32"  # 16 tiles of 64 x 64, K over 4 wave groups
     want = a.astype(np.float64) @ b.astype(np.float64)
     assert T.hybrid_error(c.reshape(256, 256), want) <= 1e-5
 
 
 @pytest.mark.parametrize("m,n,k,lda,ldb,ldc,variant", [
     (2048, 1024, 32, None, None, None, "fast"),      # 128 tiles: half the compute units
-    (1536, 2048, 96, 100, 2052, 2056, "fast"),      # padded, 16-byte aligned rows
-    (2048, 2048, 1024, None, None, None, "fast"),
-    (1024, 1024, 1024, None, None, None, "fast_t64"),  # 64 tiles of 128: 64 x 64 tiles instead
-    (192, 320, 64, 196, 324, 324, "fast_t64"),
+    (1536, 2048, 96, 100, 2052, 2056, "fast_k2"),   # padded, 16-byte aligned rows; 3 k-steps, 2 groups
+    (2048, 2048, 1024, None, None, None, "fast_k2"),  # one tile per CU: K over 2 wave groups
+    (1024, 1024, 1024, None, None, None, "fast_t64_k2"),  # 64 tiles of 128: 64 x 64 tiles instead
+    (192, 320, 64, 196, 324, 324, "fast_t64_k2"),
+    (256, 256, 160, None, None, None, "fast_t64_k4"),  # 5 k-steps over 4 wave groups
     (160, 128, 32, None, None, None, "generic"),     # M not a multiple of 64
     (2048, 2048, 30, None, None, None, "generic"),    # rows not 16-byte aligned
     (1984, 2048, 32, None, None, None, "fast_t64"),   # M a multiple of 64 only

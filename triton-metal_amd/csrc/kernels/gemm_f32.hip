@@ -76,20 +76,31 @@ TM_DEV void f_stage_b(const float *b, int64_t ldb, int k0, char *tile, int wave,
 /* AT / BT: A (B) stored transposed -- element (m, k) at k * lda + m, or
  * (k, n) at n * ldb + k.  A transposed operand's tile takes the other
  * operand's layout and reads: A^T is staged and read like B, B^T like A. */
-template <int EPI, bool AT = false, bool BT = false, int FT = 128>
+/* KG: groups of 4 waves splitting the K loop inside the workgroup (1, 2 or
+ * 4; 256 KG threads).  Group h computes k-steps h, h + KG, ... from its own
+ * double-buffered tiles; at the end groups 1 .. KG-1 leave their
+ * accumulators in LDS and group 0 adds them in order and stores.  For grids
+ * with about one workgroup per CU, this puts KG waves on every SIMD instead
+ * of one. */
+template <int EPI, bool AT = false, bool BT = false, int FT = 128, int KG = 1>
 TM_DEV void gemm_f32(const TmGemmArgs &p) {
   static_assert(!(AT && BT), "one transposed operand");
   static_assert(FT == 128 || FT == 64, "tile");
+  static_assert(KG == 1 || KG == 2 || KG == 4, "K groups");
   constexpr int FA_TILE = FT * FK * 4; /* FT rows of 128 bytes */
   constexpr int FB_TILE = FK * FT * 4; /* 32 rows of 4 FT bytes */
   constexpr int WT = FT / 2, NI = WT / 16; /* a wave's sub-tile: WT x WT, NI x NI of 16 x 16 */
-  __shared__ __align__(1024) char lds_a0[FA_TILE];
-  __shared__ __align__(1024) char lds_b0[FB_TILE];
-  __shared__ __align__(1024) char lds_a1[FA_TILE];
-  __shared__ __align__(1024) char lds_b1[FB_TILE];
+  constexpr int GROUP_BYTES = 2 * (FA_TILE + FB_TILE);
+  static_assert(KG == 1 || GROUP_BYTES >= FT * FT * 4, "a group's tiles hold its accumulators");
+  __shared__ __align__(1024) char lds[KG * GROUP_BYTES];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int kgrp = tid >> 8, wave = (tid >> 6) & 3; /* K group, wave within it */
   const int g = lane >> 4, c = lane & 15;
+  char *const lds_a0 = lds + kgrp * GROUP_BYTES;
+  char *const lds_b0 = lds_a0 + FA_TILE;
+  char *const lds_a1 = lds_b0 + FB_TILE;
+  char *const lds_b1 = lds_a1 + FA_TILE;
   const int wm = wave >> 1, wn = wave & 1; /* 2 x 2 waves */
 
   /* tile order: XCD-contiguous ranges, walked in groups of 8 tile rows */
@@ -121,14 +132,17 @@ TM_DEV void gemm_f32(const TmGemmArgs &p) {
     for (int j = 0; j < NI; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   const int ksteps = p.k / FK;
-  stage(lds_a0, lds_b0, 0);
+  if (kgrp < ksteps) stage(lds_a0, lds_b0, kgrp * FK);
   f_wait_vmem();
   __syncthreads();
 
+  /* every group meets the same barriers: the last rounds of a group with
+   * no k-step left skip the work only */
   auto step = [&](const char *ca, const char *cb, char *na, char *nb, int kb) {
-    if (kb + 1 < ksteps) {
-      stage(na, nb, (kb + 1) * FK);
+    if (kb + KG < ksteps) {
+      stage(na, nb, (kb + KG) * FK);
     }
+    if (kb < ksteps) {
 #pragma unroll
     for (int kc = 0; kc < FK / 16; ++kc) {
       /* B (first operand): element (k = 16 kc + 4g + t, column n) */
@@ -164,13 +178,36 @@ TM_DEV void gemm_f32(const TmGemmArgs &p) {
           for (int j = 0; j < NI; ++j) acc[i][j] = mfma_f32_16x16x4(bf[j][t], af[t], acc[i][j]);
       }
     }
+    }
     f_wait_vmem();
     __syncthreads();
   };
 
-  for (int kb = 0; kb < ksteps; kb += 2) {
-    step(lds_a0, lds_b0, lds_a1, lds_b1, kb);
-    if (kb + 1 < ksteps) step(lds_a1, lds_b1, lds_a0, lds_b0, kb + 1);
+  const int rounds = (ksteps + KG - 1) / KG;
+  for (int r = 0; r < rounds; r += 2) {
+    step(lds_a0, lds_b0, lds_a1, lds_b1, r * KG + kgrp);
+    if (r + 1 < rounds) step(lds_a1, lds_b1, lds_a0, lds_b0, (r + 1) * KG + kgrp);
+  }
+  if constexpr (KG > 1) {
+    /* groups 1 .. KG-1 leave their partial C^T tiles in their own LDS (the
+     * last barrier above ended every read of it); group 0 adds them */
+    auto slot = [&](int grp, int i, int j) {
+      return (f32x4 *)(lds + grp * GROUP_BYTES) + (((wave * NI + i) * NI + j) * 64 + lane);
+    };
+    if (kgrp > 0) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) *slot(kgrp, i, j) = acc[i][j];
+    }
+    __syncthreads();
+    if (kgrp > 0) return;
+#pragma unroll
+    for (int grp = 1; grp < KG; ++grp)
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] += *slot(grp, i, j);
   }
 
   /* acc[i][j] is the C^T tile: lane holds row m0 + wm*WT + i*16 + c,
@@ -209,6 +246,17 @@ extern "C" __global__ __launch_bounds__(256) void tm_gemm_fast_nt_f32(TmGemmArgs
 }
 extern "C" __global__ __launch_bounds__(256) void tm_gemm_fast_tn_f32(TmGemmArgs p) {
   gemm_f32<EPI_NONE, true, false>(p);
+}
+/* The K loop split over 2 or 4 groups of waves, for grids of about one
+ * workgroup per CU: 128 x 128 tiles at 512 threads, 64 x 64 at 512 or 1024 */
+extern "C" __global__ __launch_bounds__(512) void tm_gemm_fast_k2_f32(TmGemmArgs p) {
+  gemm_f32<EPI_NONE, false, false, 128, 2>(p);
+}
+extern "C" __global__ __launch_bounds__(512) void tm_gemm_fast_t64_k2_f32(TmGemmArgs p) {
+  gemm_f32<EPI_NONE, false, false, 64, 2>(p);
+}
+extern "C" __global__ __launch_bounds__(1024) void tm_gemm_fast_t64_k4_f32(TmGemmArgs p) {
+  gemm_f32<EPI_NONE, false, false, 64, 4>(p);
 }
 /* 64 x 64 tiles (4 waves of 32 x 32) for problems with too few 128 x 128 tiles */
 extern "C" __global__ __launch_bounds__(256) void tm_gemm_fast_t64_f32(TmGemmArgs p) {

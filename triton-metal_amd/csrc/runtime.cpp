@@ -632,10 +632,20 @@ void choose_gemm(Plan &plan, const TmGemmArgs &p, const BuiltinSpec &spec, const
     const bool b_t = gemm && !b_n && p.sbk == 1 && p.sbn % 4 == 0 && p.sbn >= p.k;
     if ((a_n || a_t) && (b_n || b_t) && !(a_t && b_t)) {
       const int tile = f32_big ? 128 : 64;
-      plan.variant = format("tm_%s_fast%s%s_f32", family, b_t ? "_nt" : a_t ? "_tn" : "",
-                            f32_big ? "" : "_t64");
-      plan.grid[0] = (unsigned)((p.m / tile) * (p.n / tile));
-      plan.block = 256;
+      const int64_t tiles = (int64_t)(p.m / tile) * (p.n / tile);
+      /* About one workgroup per CU or fewer (one wave per SIMD): split the K
+       * loop over 2 (128 x 128 tiles) or up to 4 (64 x 64) groups of waves
+       * inside the workgroup (plain row-major matmul only) */
+      int64_t kg = 1;
+      if (gemm && a_n && b_n) {
+        const int64_t cus = std::max(device().compute_units, 1);
+        kg = std::min<int64_t>({2 * cus / std::max<int64_t>(tiles, 1), f32_big ? 2 : 4, p.k / 32});
+        kg = kg >= 4 ? 4 : kg >= 2 ? 2 : 1;
+      }
+      plan.variant = format("tm_%s_fast%s%s%s_f32", family, b_t ? "_nt" : a_t ? "_tn" : "",
+                            f32_big ? "" : "_t64", kg > 1 ? (kg == 4 ? "_k4" : "_k2") : "");
+      plan.grid[0] = (unsigned)tiles;
+      plan.block = (unsigned)(256 * kg);
       return;
     }
   }
