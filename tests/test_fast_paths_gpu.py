@@ -187,29 +187,38 @@ def _gemm(m, n, k, element, lda=None, ldb=None, ldc=None, seed=0, poison=False, 
     return c, want, variant
 
 
-def _tile_suffix(m, n, cus=256):
+def _tile_suffix(m, n, cus=256, k=None):
     """The planner's tile choice on an MI355X (256 compute units): rounds of
     resident 256 x 256 tiles (one per CU) at 31 against rounds of 128 x 128
     pairs (two per CU) at 21; with fewer 128 x 128 tiles than CUs, 64 x 64
-    tiles ("_t64")."""
+    tiles ("_t64").  Given k (whole row-major tiles only), fewer smaller
+    tiles than two per CU and k >= 128 also split the K loop over wave
+    groups ("_k2" for 128 x 128, "_k4" for 64 x 64)."""
     cd = lambda a, b: -(-a // b)
     big = cd(cd(m, 256) * cd(n, 256), cus) * 31 <= cd(cd(m, 128) * cd(n, 128), 2 * cus) * 21
     if big:
         return ""
-    return "_t64" if cd(m, 128) * cd(n, 128) < cus else "_t128"
+    small = cd(m, 128) * cd(n, 128) < cus
+    tile = 64 if small else 128
+    suffix = "_t64" if small else "_t128"
+    if k is not None and k >= 128 and cd(m, tile) * cd(n, tile) < 2 * cus:
+        suffix += "_k4" if small else "_k2"
+    return suffix
 @pytest.mark.parametrize("element", ["bf16", "f16"])
 @pytest.mark.parametrize("m,n,k,lda,ldb,ldc,tile", [
     (256, 512, 64, None, None, None, "_t64"),
-    (512, 256, 192, None, None, None, "_t64"),
-    (768, 1024, 320, 328, 1032, 1040, "_t64"),    # padded leading dimensions, 16-byte aligned
+    (512, 256, 192, None, None, None, "_t64_k4"),   # 3 k-steps over 4 wave groups
+    (768, 1024, 320, 328, 1032, 1040, "_t64_k4"),  # padded leading dimensions, 16-byte aligned
     (2048, 2048, 64, None, None, None, "_t128"),
-    (2560, 2048, 128, 136, 2056, 2052, "_t128"),
+    (2560, 2048, 128, 136, 2056, 2052, "_t128_k2"),
+    (2048, 2048, 2048, None, None, None, "_t128_k2"),
+    (1024, 1024, 1024, None, None, None, "_t64_k4"),
     (4096, 4096, 128, None, None, None, ""),
     (4096, 4096, 64, 72, 4104, 4100, ""),
 ])
 def test_fast_gemm_shapes_and_strides(element, m, n, k, lda, ldb, ldc, tile, device):
     c, want, variant = _gemm(m, n, k, element, lda, ldb, ldc)
-    assert tile == _tile_suffix(m, n)
+    assert tile == _tile_suffix(m, n, k=k)
     assert variant == f"tm_gemm_fast{tile}_{element}"
     assert T.hybrid_error(c[:, :n], want) <= 2e-2
     if ldc:
@@ -364,7 +373,7 @@ def test_gemm_layout_sweep(m, n, k, layout, pk, pn, pm, element, device):
     (256, 256, 60, None, None, "generic"),    # rows of A not 16-byte aligned
     (300, 200, 100, None, None, "generic"),
     (255, 256, 64, None, None, "ragged_t64"),
-    (512, 256, 128, None, None, "fast_t64"),
+    (512, 256, 128, None, None, "fast_t64_k4"),
     (2048, 2048, 64, None, None, "fast_t128"),
     (2000, 2100, 72, None, 2104, "ragged_t128"),
     (4096, 4096, 64, None, None, "fast"),

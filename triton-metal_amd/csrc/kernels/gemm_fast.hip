@@ -200,7 +200,14 @@ TM_DEV uint32_t g_pack2(float lo, float hi) {
  * AT: A is stored transposed (element (m, k) at k * lda + m, the layout of
  * dY^T X in a linear layer's weight gradient).  Its tile is then [64 x BM]
  * m-contiguous like B's, copied and read the same way (transposed reads). */
-template <typename T, int EPI, bool RAGGED, int BM, int BN, bool BT = false, bool AT = false>
+/* KG: groups of 2 WN waves splitting the K loop inside the workgroup (1, 2
+ * or 4; whole tiles only).  Group h contracts k-steps h, h + KG, ... from its
+ * own double-buffered tiles; at the end groups 1 .. KG-1 leave their
+ * accumulators in LDS and group 0 adds them in order and stores.  For grids
+ * of about one workgroup per CU (128 x 128 tiles at 2048^3, 64 x 64 at
+ * 1024^3), this puts more waves on every SIMD. */
+template <typename T, int EPI, bool RAGGED, int BM, int BN, bool BT = false, bool AT = false,
+          int KG = 1>
 TM_DEV void gemm_fast(const TmGemmArgs &p) {
   typedef typename GVec8<T>::type v8;
   constexpr int GBM = BM, GBN = BN;
@@ -210,14 +217,19 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   constexpr int MI = BM / 32;          /* 16-row tiles per wave */
   static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 128) || (BM == 64 && BN == 64),
                 "tile shapes");
-  __shared__ __align__(1024) char lds_a0[A_TILE];
-  __shared__ __align__(1024) char lds_b0[B_TILE];
-  __shared__ __align__(1024) char lds_a1[A_TILE];
-  __shared__ __align__(1024) char lds_b1[B_TILE];
-
+  constexpr int GROUP_BYTES = 2 * (A_TILE + B_TILE);
+  static_assert(KG == 1 || (!RAGGED && GROUP_BYTES >= 2 * WN * MI * 4 * 64 * 16),
+                "K groups: whole tiles, and a group's tiles hold its accumulators");
   const int tid = threadIdx.x, lane = tid & 63;
+  const int kgrp = KG == 1 ? 0 : (tid >> 6) / (2 * WN); /* K group */
+  /* the kernel body over its LDS: one workgroup-wide group takes four
+   * separate tile arrays (the compiler then knows they do not alias), K
+   * groups one array carved per group (`lds`, also where the groups'
+   * accumulators meet) */
+  auto body = [&](char *const lds_a0, char *const lds_b0, char *const lds_a1, char *const lds_b1,
+                  char *const lds) __attribute__((always_inline)) {
   /* uniform in the ragged kernel, whose copy ranges are scalar arithmetic */
-  const int wave = RAGGED ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
+  const int wave = RAGGED ? __builtin_amdgcn_readfirstlane(tid >> 6) : KG == 1 ? tid >> 6 : (tid >> 6) % (2 * WN);
   const int g = lane >> 4, c = lane & 15;
   const int wm = wave / WN, wn = wave % WN; /* 2 x WN waves */
 
@@ -269,7 +281,7 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
     for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   const int ksteps = (p.k + GBK - 1) / GBK;
-  stage(lds_a0, lds_b0, 0);
+  if (kgrp < ksteps) stage(lds_a0, lds_b0, kgrp);
   g_wait_vmem();
   __syncthreads();
 
@@ -278,9 +290,10 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
    * the range check. */
   auto step = [&](auto last_tag, const char *ca, const char *cb, char *na, char *nb, int kb) {
     constexpr bool LAST = decltype(last_tag)::value;
-    if (!LAST && kb + 1 < ksteps) stage(na, nb, kb + 1);
+    if (!LAST && kb + KG < ksteps) stage(na, nb, kb + KG);
+    /* a group with no k-step left in the last round still meets its barrier */
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < 2 && (KG == 1 || kb < ksteps); ++ks) {
       v8 bf[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -320,13 +333,40 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
 
   /* with a ragged K the last step runs masked */
   const int kfull = RAGGED && p.k % GBK ? ksteps - 1 : ksteps;
-  for (int kb = 0; kb < kfull; kb += 2) {
-    step(Full{}, lds_a0, lds_b0, lds_a1, lds_b1, kb);
-    if (kb + 1 < kfull) step(Full{}, lds_a1, lds_b1, lds_a0, lds_b0, kb + 1);
-  }
-  if (RAGGED && kfull < ksteps) {
-    const bool odd = kfull & 1;
-    step(Last{}, odd ? lds_a1 : lds_a0, odd ? lds_b1 : lds_b0, nullptr, nullptr, kfull);
+  if constexpr (KG == 1) {
+    for (int kb = 0; kb < kfull; kb += 2) {
+      step(Full{}, lds_a0, lds_b0, lds_a1, lds_b1, kb);
+      if (kb + 1 < kfull) step(Full{}, lds_a1, lds_b1, lds_a0, lds_b0, kb + 1);
+    }
+    if (RAGGED && kfull < ksteps) {
+      const bool odd = kfull & 1;
+      step(Last{}, odd ? lds_a1 : lds_a0, odd ? lds_b1 : lds_b0, nullptr, nullptr, kfull);
+    }
+  } else {
+    const int rounds = (ksteps + KG - 1) / KG;
+    for (int r = 0; r < rounds; r += 2) {
+      step(Full{}, lds_a0, lds_b0, lds_a1, lds_b1, r * KG + kgrp);
+      if (r + 1 < rounds) step(Full{}, lds_a1, lds_b1, lds_a0, lds_b0, (r + 1) * KG + kgrp);
+    }
+    /* groups 1 .. KG-1 leave their partial C^T tiles in their own LDS (the
+     * last barrier above ended every read of it); group 0 adds them */
+    auto slot = [&](int grp, int i, int j) {
+      return (f32x4 *)(lds + grp * GROUP_BYTES) + (((wave * MI + i) * 4 + j) * 64 + lane);
+    };
+    if (kgrp > 0) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *slot(kgrp, i, j) = acc[i][j];
+    }
+    __syncthreads();
+    if (kgrp > 0) return;
+#pragma unroll
+    for (int grp = 1; grp < KG; ++grp)
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += *slot(grp, i, j);
   }
 
   /* acc[i][j] is the C^T tile: lane holds row m0 + wm*BM/2 + i*16 + c,
@@ -365,12 +405,34 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
       }
     }
   }
+  };
+  if constexpr (KG == 1) {
+    __shared__ __align__(1024) char tile_a0[A_TILE];
+    __shared__ __align__(1024) char tile_b0[B_TILE];
+    __shared__ __align__(1024) char tile_a1[A_TILE];
+    __shared__ __align__(1024) char tile_b1[B_TILE];
+    body(tile_a0, tile_b0, tile_a1, tile_b1, nullptr);
+  } else {
+    __shared__ __align__(1024) char lds[KG * GROUP_BYTES];
+    char *const mine = lds + kgrp * GROUP_BYTES;
+    body(mine, mine + A_TILE, mine + A_TILE + B_TILE, mine + 2 * A_TILE + B_TILE, lds);
+  }
 }
 
 #define TM_GEMM_ONE(NAME, T, EPI, RAGGED, TILE, BT, AT)                                     \
   extern "C" __global__ __launch_bounds__(TILE * 2) void NAME(TmGemmArgs p) {                 \
     gemm_fast<T, EPI, RAGGED, TILE, TILE, BT, AT>(p);                                          \
   }
+/* whole 128 x 128 (64 x 64) tiles, row-major, the K loop over 2 (4) wave groups */
+#define TM_GEMM_KSPLIT(T, TN)                                                                   \
+  extern "C" __global__ __launch_bounds__(512) void tm_gemm_fast_t128_k2_##TN(TmGemmArgs p) {   \
+    gemm_fast<T, EPI_NONE, false, 128, 128, false, false, 2>(p);                                \
+  }                                                                                             \
+  extern "C" __global__ __launch_bounds__(512) void tm_gemm_fast_t64_k4_##TN(TmGemmArgs p) {    \
+    gemm_fast<T, EPI_NONE, false, 64, 64, false, false, 4>(p);                                  \
+  }
+TM_GEMM_KSPLIT(bf16_t, bf16)
+TM_GEMM_KSPLIT(f16_t, f16)
 #define TM_GEMM_FAST(T, TN)                                                       \
   TM_GEMM_ONE(tm_gemm_fast_##TN, T, EPI_NONE, false, 256, false, false)           \
   TM_GEMM_ONE(tm_gemm_ragged_##TN, T, EPI_NONE, true, 256, false, false)          \

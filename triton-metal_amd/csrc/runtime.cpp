@@ -676,10 +676,16 @@ void choose_gemm(Plan &plan, const TmGemmArgs &p, const BuiltinSpec &spec, const
     const bool small = !big && cdiv(p.m, 128) * cdiv(p.n, 128) < cus;
     const int tile = big ? 256 : small ? 64 : 128;
     const bool whole = p.m % tile == 0 && p.n % tile == 0 && p.k % 64 == 0;
-    plan.variant = format("tm_%s_%s%s%s_%s", family, whole ? "fast" : "ragged",
-                          nt ? "_nt" : tn ? "_tn" : "", big ? "" : small ? "_t64" : "_t128", el);
-    plan.grid[0] = (unsigned)(cdiv(p.m, tile) * cdiv(p.n, tile));
-    plan.block = (unsigned)(2 * tile);
+    const int64_t tiles = cdiv(p.m, tile) * cdiv(p.n, tile);
+    /* whole row-major tiles with fewer 128 x 128 workgroups than two per CU
+     * (one wave per SIMD), or 64 x 64 ones (two waves per CU): the K loop
+     * split over 2 or 4 wave groups inside the workgroup, 512 threads */
+    const bool ksplit = TM_GEMM_KSPLIT && gemm && nn && whole && !big && p.k >= 128 && tiles < 2 * cus;
+    plan.variant = format("tm_%s_%s%s%s%s_%s", family, whole ? "fast" : "ragged",
+                          nt ? "_nt" : tn ? "_tn" : "", big ? "" : small ? "_t64" : "_t128",
+                          ksplit ? (small ? "_k4" : "_k2") : "", el);
+    plan.grid[0] = (unsigned)tiles;
+    plan.block = (unsigned)(ksplit ? 512 : 2 * tile);
   } else {
     plan.variant = format("tm_%s_generic_%s", family, el);
     plan.grid[0] = (unsigned)cdiv(p.m, 64);
@@ -795,6 +801,9 @@ void plan_stash_backward(Plan &plan, const BuiltinSpec &spec, const TmAttnDkdvAr
 /* Ranges to split a generic attention kernel's walk into when its grid of
  * `wgs` 64-row workgroups cannot fill the chip twice: enough to (at most 16,
  * each at least two 32-row blocks of the `n_ctx` walked); 1 for no split. */
+#ifndef TM_GEMM_KSPLIT
+#define TM_GEMM_KSPLIT 1
+#endif
 int64_t split_ranges(int64_t wgs, int64_t n_ctx) {
   const int64_t cus = std::max(device().compute_units, 1);
   if (wgs >= 2 * cus) return 1;
