@@ -6,6 +6,12 @@ the nominal 2.4 GHz and as totals, so they compare directly with the MI355X
 published peaks (256 CUs; dense bf16 MFMA 2.5 PFLOP/s = 4096 FLOP/clk/CU).
 
   mfma_16x16x32 / mfma_32x32x16   back-to-back bf16 MFMAs, 4 independent chains
+  gemm_wave_mfma_16x16x32 / _32x32x16
+                                  the MFMA stream of the bf16 GEMM's wave (a
+                                  128 x 64 sub-tile, 64 k per step, 8 waves =
+                                  2 per SIMD) with operand bits changing every
+                                  step, no memory: the issue ceiling a GEMM of
+                                  that shape can reach
   exp2                            v_exp_f32 throughput
   lds_b128 / lds_tr_b64           ds_read_b128 and ds_read_b64_tr_b16 bytes, on
                                   conflict-free addresses
@@ -119,6 +125,59 @@ extern "C" __global__ __launch_bounds__(256) void probe_lds_tr(unsigned *out, in
   if (acc[0] == 0x12345678u) out[0] = acc[1];
 }
 
+/* The GEMM wave's MFMA stream: 32 accumulators of 16 x 16 (or 8 of 32 x 32)
+ * for a 128 x 64 sub-tile, 64 k per iteration; operands from registers,
+ * stepped by an add each iteration so their bits (and the power drawn) move
+ * as with real data. */
+extern "C" __global__ __launch_bounds__(512) void probe_gemm_wave16(float *out, int iters) {
+  const unsigned seed = 12345u + threadIdx.x;
+  f32x4 acc[8][4] = {};
+  u32x4 a[8], b[4];
+  for (int i = 0; i < 8; ++i) a[i] = (u32x4){seed * (i + 1), seed + i, seed ^ 0x5a5a1234u, seed * 7u + i};
+  for (int j = 0; j < 4; ++j) b[j] = (u32x4){seed * (j + 3), seed - j, seed ^ 0x3c3c4321u, seed * 5u + j};
+  for (int it = 0; it < iters; ++it)
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, b[j]),
+                                                              __builtin_bit_cast(bf16x8, a[i]), acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] += 0x9e3779b9u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] += 0x7f4a7c15u;
+    }
+  float s = 0;
+  for (int i = 0; i < 8; ++i)
+    for (int j = 0; j < 4; ++j) s += acc[i][j][0] + acc[i][j][3];
+  if (s == 1234.5f) out[0] = 1;
+}
+extern "C" __global__ __launch_bounds__(512) void probe_gemm_wave32(float *out, int iters) {
+  const unsigned seed = 12345u + threadIdx.x;
+  f32x16 acc[4][2] = {};
+  u32x4 a[4], b[2];
+  for (int i = 0; i < 4; ++i) a[i] = (u32x4){seed * (i + 1), seed + i, seed ^ 0x5a5a1234u, seed * 7u + i};
+  for (int j = 0; j < 2; ++j) b[j] = (u32x4){seed * (j + 3), seed - j, seed ^ 0x3c3c4321u, seed * 5u + j};
+  for (int it = 0; it < iters; ++it)
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, b[j]),
+                                                              __builtin_bit_cast(bf16x8, a[i]), acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] += 0x9e3779b9u;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] += 0x7f4a7c15u;
+    }
+  float s = 0;
+  for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 2; ++j) s += acc[i][j][0] + acc[i][j][15];
+  if (s == 1234.5f) out[0] = 1;
+}
+
 /* Each workgroup adds into one [32 x 128] fp32 tile of a 64 MiB buffer `iters`
  * times: with atomics, or as a plain read-add-write. */
 extern "C" __global__ __launch_bounds__(256) void probe_atomic(float *acc, int iters) {
@@ -177,11 +236,34 @@ def run(iters=4096, workgroups=CUS * 16):
                              "total_per_s": float(f"{total:.4g}"),
                              "per_cu_clk": round(total / CUS / CLOCK_HZ, 2)}
             _core.release_kernel(kernel)
+        results.update(_gemm_wave_mfma(lib))
         results["atomic_dq_config5"] = _dq_atomics(lib)
     finally:
         _core.free_buffer(scratch)
         _core.release_library(lib)
     return results
+
+
+def _gemm_wave_mfma(lib, iters=2048, workgroups=CUS * 4):
+    """The GEMM wave's MFMA stream at the GEMM's occupancy: 512-thread
+    workgroups, 8 waves of 128 x 64 x 64 per iteration."""
+    out = {}
+    scratch = _core.alloc_buffer(4096)
+    try:
+        for name, kernel_name in (("gemm_wave_mfma_16x16x32_bf16", "probe_gemm_wave16"),
+                                  ("gemm_wave_mfma_32x32x16_bf16", "probe_gemm_wave32")):
+            kernel = _core.load_kernel(lib, kernel_name)
+            grid = (workgroups, 1, 1)
+            args = ([_core.ARG_BUFFER, _core.ARG_I32], [scratch, iters])
+            _core.launch(kernel, grid, 512, *args)
+            ms = _core.launch_timed(kernel, grid, 512, args[0], args[1], 5) / 5
+            total = workgroups * iters * 8 * 128 * 64 * 64 * 2 / (ms * 1e-3)
+            out[name] = {"ms": round(ms, 4), "unit": "FLOP", "total_per_s": float(f"{total:.4g}"),
+                         "per_cu_clk": round(total / CUS / CLOCK_HZ, 2)}
+            _core.release_kernel(kernel)
+    finally:
+        _core.free_buffer(scratch)
+    return out
 
 
 def _dq_atomics(lib, heads=128, seq=4096):
