@@ -603,6 +603,11 @@ void validate_attn_common(const char *name, int64_t heads, int32_t stride_head,
   if (heads > 65535) throw TmError(format("%s: %lld heads exceeds 65535", name, (long long)heads));
 }
 
+/* 0 turns the bf16/f16 GEMM's intra-workgroup K split off (measurement builds) */
+#ifndef TM_GEMM_KSPLIT
+#define TM_GEMM_KSPLIT 1
+#endif
+
 /* Kernel choice shared by matmul_kernel and sae_encode_kernel.  The
  * specialised kernels take 16-bit elements and row-major operands with unit
  * inner stride, 16-byte aligned rows of A and B, 8-byte aligned rows of C,
@@ -801,9 +806,6 @@ void plan_stash_backward(Plan &plan, const BuiltinSpec &spec, const TmAttnDkdvAr
 /* Ranges to split a generic attention kernel's walk into when its grid of
  * `wgs` 64-row workgroups cannot fill the chip twice: enough to (at most 16,
  * each at least two 32-row blocks of the `n_ctx` walked); 1 for no split. */
-#ifndef TM_GEMM_KSPLIT
-#define TM_GEMM_KSPLIT 1
-#endif
 int64_t split_ranges(int64_t wgs, int64_t n_ctx) {
   const int64_t cus = std::max(device().compute_units, 1);
   if (wgs >= 2 * cus) return 1;
