@@ -686,7 +686,9 @@ TM_PRE_FAST(f16_t, f16, 128)
  *   P^T  = exp2(qk_scale S^T - L), dS^T = P^T (dP^T - Delta)
  *   dQ^T += K^T dS^T                       (K^T: ds_read_b64_tr_b16 of the K tile)
  * dS is rounded to the element type before its dot, as the reference does
- * (AttentionBackwardKernel.swift:155-160). */
+ * (AttentionBackwardKernel.swift:155-160).  The dP^T MFMAs start from -Delta
+ * (a lane's four values share its query) instead of zero, so they deliver
+ * dP^T - Delta with no subtraction per element. */
 template <typename T, int D, bool CAUSAL>
 TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
   constexpr int BM = 128, BN = 64, QW = 32;
@@ -743,6 +745,8 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
     dlt[qt] = Dg[qi];
   }
   const float qk_scale = p.sm_scale * TM_LOG2E;
+  const f32x4 ndlt[2] = {(f32x4){-dlt[0], -dlt[0], -dlt[0], -dlt[0]},
+                         (f32x4){-dlt[1], -dlt[1], -dlt[1], -dlt[1]}};
   f32x4 acc[D / 16][2];
 #pragma unroll
   for (int dt = 0; dt < D / 16; ++dt) acc[dt][0] = acc[dt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -765,7 +769,9 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int kt = 2 * kk + h;
-        s[h][0] = s[h][1] = dp[h][0] = dp[h][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        s[h][0] = s[h][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        dp[h][0] = ndlt[0];
+        dp[h][1] = ndlt[1];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           const v8 ka = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D>(kt * 16 + c, ks * 4 + g)));
@@ -791,7 +797,7 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
               const int key = k0 + (2 * kk + h) * 16 + 4 * g + r;
               x = (key >= n || (CAUSAL && key > qi)) ? TM_NEG_INF : x;
             }
-            ds[h][r] = fast_exp2(x) * (dp[h][qt][r] - dlt[qt]);
+            ds[h][r] = fast_exp2(x) * dp[h][qt][r];
           }
         dsf[qt] = (u32x4){pack2<T>(ds[0][0], ds[0][1]), pack2<T>(ds[0][2], ds[0][3]),
                           pack2<T>(ds[1][0], ds[1][1]), pack2<T>(ds[1][2], ds[1][3])};
@@ -845,6 +851,7 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
  *   S  = Q K^T, dP = dO V^T                (Q, dO: ds_read_b128 of the tiles)
  *   P  = exp2(qk_scale S - L), dS = P (dP - Delta)
  *   dV^T += dO^T P, dK^T += Q^T dS         (dO^T, Q^T: ds_read_b64_tr_b16)
+ * (the split kernel carries -dS, see NEGV below)
  * P and dS are rounded to the element type before their dots
  * (AttentionBackwardKernel.swift:357-369).  Causal: the heaviest key blocks
  * (lowest keys) run first and the query walk starts at the block's first key.
@@ -863,6 +870,10 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
    * per softmax pass; measured 7% faster), 32 at D = 128, where 64 would not
    * fit the registers */
   constexpr int BN = 128, KW = 32, BM = D == 64 ? 64 : 32;
+  /* the split kernel computes -dS = P (Delta - dP), with the dP MFMAs on -V
+   * and started from Delta (no subtraction per element), accumulates -dK and
+   * flips the sign at the store; the fused forms keep dS itself */
+  constexpr bool NEGV = !FUSED && !STASH;
   constexpr int QT = BM / 16, KK = BM / 32;
   constexpr int KS = D / 32;
   constexpr int TILE = BM * D * 2;
@@ -921,6 +932,8 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
     for (int ks = 0; ks < KS; ++ks) {
       kf[kt][ks] = *(const u32x4 *)(Kg + (int64_t)key * ss + ks * 32 + 8 * g);
       vf[kt][ks] = *(const u32x4 *)(Vg + (int64_t)key * ss + ks * 32 + 8 * g);
+      /* NEGV: -V, every element's sign bit flipped (exact) */
+      if constexpr (NEGV) vf[kt][ks] ^= (u32x4){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
     }
   }
   /* FUSED: K as the B operand of dQ[:, wave's D/4 columns] = dS K, for the
@@ -948,6 +961,7 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
       }
   }
   const float qk_scale = p.sm_scale * TM_LOG2E;
+  const float dk_scale = NEGV ? -p.sm_scale : p.sm_scale;
   f32x4 dk[D / 16][2], dv[D / 16][2];
 #pragma unroll
   for (int dt = 0; dt < D / 16; ++dt)
@@ -969,7 +983,9 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
     f32x4 s[2][QT], dp[2][QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      s[0][qt] = s[1][qt] = dp[0][qt] = dp[1][qt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      s[0][qt] = s[1][qt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      /* NEGV: Delta - dP, from Delta (-V above) */
+      dp[0][qt] = dp[1][qt] = NEGV ? dlt[qt] : (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const v8 qa = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D>(qt * 16 + c, ks * 4 + g)));
@@ -996,7 +1012,7 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
             x = (qi >= n || (CAUSAL && qi < key)) ? TM_NEG_INF : x;
           }
           pr[qt][r] = fast_exp2(x);
-          ds[qt][r] = pr[qt][r] * (dp[kt][qt][r] - dlt[qt][r]);
+          ds[qt][r] = NEGV ? pr[qt][r] * dp[kt][qt][r] : pr[qt][r] * (dp[kt][qt][r] - dlt[qt][r]);
         }
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
@@ -1212,8 +1228,8 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) {
         u32x2 wk, wv;
-        wk[0] = pack2<T>(dk[dt][kt][0] * p.sm_scale, dk[dt][kt][1] * p.sm_scale);
-        wk[1] = pack2<T>(dk[dt][kt][2] * p.sm_scale, dk[dt][kt][3] * p.sm_scale);
+        wk[0] = pack2<T>(dk[dt][kt][0] * dk_scale, dk[dt][kt][1] * dk_scale);
+        wk[1] = pack2<T>(dk[dt][kt][2] * dk_scale, dk[dt][kt][3] * dk_scale);
         wv[0] = pack2<T>(dv[dt][kt][0], dv[dt][kt][1]);
         wv[1] = pack2<T>(dv[dt][kt][2], dv[dt][kt][3]);
         *(u32x2 *)(dKg + (int64_t)key * ss + dt * 16 + 4 * g) = wk;
