@@ -851,7 +851,7 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
  *   S  = Q K^T, dP = dO V^T                (Q, dO: ds_read_b128 of the tiles)
  *   P  = exp2(qk_scale S - L), dS = P (dP - Delta)
  *   dV^T += dO^T P, dK^T += Q^T dS         (dO^T, Q^T: ds_read_b64_tr_b16)
- * (the split kernel carries -dS, see NEGV below)
+ * (carried as -dS, see below)
  * P and dS are rounded to the element type before their dots
  * (AttentionBackwardKernel.swift:357-369).  Causal: the heaviest key blocks
  * (lowest keys) run first and the query walk starts at the block's first key.
@@ -870,10 +870,10 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
    * per softmax pass; measured 7% faster), 32 at D = 128, where 64 would not
    * fit the registers */
   constexpr int BN = 128, KW = 32, BM = D == 64 ? 64 : 32;
-  /* the split kernel computes -dS = P (Delta - dP), with the dP MFMAs on -V
-   * and started from Delta (no subtraction per element), accumulates -dK and
-   * flips the sign at the store; the fused forms keep dS itself */
-  constexpr bool NEGV = !FUSED && !STASH;
+  /* The kernel carries -dS = P (Delta - dP): the dP MFMAs run on -V and start
+   * from Delta, so no subtraction per element.  dK accumulates -dK and flips
+   * the sign at the store; FUSED adds dQ with -K, STASH stores -dS and its dQ
+   * pass flips the sign. */
   constexpr int QT = BM / 16, KK = BM / 32;
   constexpr int KS = D / 32;
   constexpr int TILE = BM * D * 2;
@@ -932,8 +932,8 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
     for (int ks = 0; ks < KS; ++ks) {
       kf[kt][ks] = *(const u32x4 *)(Kg + (int64_t)key * ss + ks * 32 + 8 * g);
       vf[kt][ks] = *(const u32x4 *)(Vg + (int64_t)key * ss + ks * 32 + 8 * g);
-      /* NEGV: -V, every element's sign bit flipped (exact) */
-      if constexpr (NEGV) vf[kt][ks] ^= (u32x4){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+      /* -V: every element's sign bit flipped (exact) */
+      vf[kt][ks] ^= (u32x4){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
     }
   }
   /* FUSED: K as the B operand of dQ[:, wave's D/4 columns] = dS K, for the
@@ -956,12 +956,14 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
           const int key = k0 + ks * 32 + (j < 4 ? 4 * g + j : 16 + 4 * g + j - 4);
           h[j] = key < n ? Kh[(int64_t)key * ss + col] : 0u;
         }
+        /* -K (sign bits flipped, exact): dS K = (-dS)(-K) */
         kq[ks][nt] = (u32x4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                             h[6] | (h[7] << 16)};
+                             h[6] | (h[7] << 16)} ^
+                     (u32x4){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
       }
   }
   const float qk_scale = p.sm_scale * TM_LOG2E;
-  const float dk_scale = NEGV ? -p.sm_scale : p.sm_scale;
+  const float dk_scale = -p.sm_scale; /* dk holds -dK / sm_scale */
   f32x4 dk[D / 16][2], dv[D / 16][2];
 #pragma unroll
   for (int dt = 0; dt < D / 16; ++dt)
@@ -984,8 +986,8 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       s[0][qt] = s[1][qt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-      /* NEGV: Delta - dP, from Delta (-V above) */
-      dp[0][qt] = dp[1][qt] = NEGV ? dlt[qt] : (f32x4){0.f, 0.f, 0.f, 0.f};
+      /* Delta - dP: started from Delta, on -V */
+      dp[0][qt] = dp[1][qt] = dlt[qt];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const v8 qa = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D>(qt * 16 + c, ks * 4 + g)));
@@ -1012,7 +1014,7 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
             x = (qi >= n || (CAUSAL && qi < key)) ? TM_NEG_INF : x;
           }
           pr[qt][r] = fast_exp2(x);
-          ds[qt][r] = NEGV ? pr[qt][r] * dp[kt][qt][r] : pr[qt][r] * (dp[kt][qt][r] - dlt[qt][r]);
+          ds[qt][r] = pr[qt][r] * dp[kt][qt][r]; /* -dS */
         }
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
@@ -1250,8 +1252,8 @@ TM_DEV int stash_pos(int q) {
 
 /* ---- backward: dQ from a dS stash (bwd=stash) ----------------------------
  * dQ = dS K without recomputing S and dP: the dK/dV kernel's stash form wrote
- * dS^T (rounded to the element type, as the split dq kernel rounds it before
- * its dot) as [query block of 32][stash_keys][32 queries in stash_pos order].
+ * -dS^T (rounded to the element type, as the split dq kernel rounds dS before
+ * its dot; the sign is flipped at the store) as [query block of 32][stash_keys][32 queries in stash_pos order].
  * One workgroup = 8 waves = 256 queries (one workgroup per CU), the key
  * blocks (64 keys) of its head up to the last one its queries see; per block
  * the K tile and a [64 keys][256 queries] dS^T tile (two halves of 128,
@@ -1412,8 +1414,9 @@ TM_DEV void attn_dq_stash(const TmAttnFusedArgs &a) {
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) {
         u32x2 w;
-        w[0] = pack2<T>(acc[dt][qt][0] * p.sm_scale, acc[dt][qt][1] * p.sm_scale);
-        w[1] = pack2<T>(acc[dt][qt][2] * p.sm_scale, acc[dt][qt][3] * p.sm_scale);
+        /* the stash holds -dS */
+        w[0] = pack2<T>(acc[dt][qt][0] * -p.sm_scale, acc[dt][qt][1] * -p.sm_scale);
+        w[1] = pack2<T>(acc[dt][qt][2] * -p.sm_scale, acc[dt][qt][3] * -p.sm_scale);
         *(u32x2 *)(dQg + (int64_t)qi * ss + dt * 16 + 4 * g) = w;
       }
     }
