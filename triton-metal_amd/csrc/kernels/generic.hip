@@ -134,22 +134,41 @@ struct TileStager {
       bs[(e / DP) * (DP + 1) + e % DP] = rb[i];
     }
   }
+  /* the forward's layouts: a row-major with 16-byte aligned rows of DP + 4,
+   * b transposed ([DP][ROWS + 4]), so a lane's four consecutive d (of a) or
+   * keys (of b) are one 16-byte read */
+  TM_DEV void store_rows_cols(float *as, float *bt, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + 256 * i;
+      as[(e / DP) * (DP + 4) + e % DP] = ra[i];
+      bt[(e % DP) * (ROWS + 4) + e / DP] = rb[i];
+    }
+  }
 };
 
 /* ---------------------------------------------------------------------------
  * attn_fwd: FlashAttention-2 forward with the online softmax in the exp2
  * domain (AttentionKernel.swift:40-250; attention_training.py:37-71).
- * 64 queries per workgroup (16 per wave), keys in blocks of 32.
+ * 64 queries per workgroup (16 per wave), keys in blocks of 64 (32 at DP = 96 and 128).
  * Each wave computes S^T = K Q^T so that a lane owns one query (column l%16)
  * and four keys per 16-key tile; the row statistics are then lane-local up to
  * a reduction over the four lane groups, and O^T = V^T P^T keeps the same
  * lane <-> query ownership for the rescale.
+ * Operands come four MFMAs at a time from one 16-byte LDS read: the S^T
+ * contraction takes d in the order 16 j + 4 g + t (lane group g, MFMA t of
+ * chunk j), so a lane reads K[key][16 j + 4 g .. +3] at once and Q holds the
+ * same d order; V is staged transposed, so the four keys 4 g + m of MFMAs
+ * m = 0..3 of a P V step are adjacent in a V^T row.
  * ------------------------------------------------------------------------- */
 template <typename T, int DP, bool CAUSAL>
 TM_DEV void attn_fwd_generic(const TmAttnFwdArgs &p) {
-  constexpr int BM = 64, BN = 32, LD = DP + 1;
-  __shared__ float Ks[BN * LD];
-  __shared__ float Vs[BN * LD];
+  /* 64-key blocks; 32 at DP = 96 and 128, where the staged tiles and the
+   * operands of 64 keys would need more registers than two waves per SIMD
+   * leave */
+  constexpr int BM = 64, BN = DP >= 96 ? 32 : 64, LDK = DP + 4, LDV = BN + 4, KT = BN / 16;
+  __shared__ __align__(16) float Ks[BN * LDK];
+  __shared__ __align__(16) float Vt[DP * LDV];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c = lane & 15;
   const int bh = blockIdx.y;
@@ -162,12 +181,14 @@ TM_DEV void attn_fwd_generic(const TmAttnFwdArgs &p) {
   T *O = (T *)p.o + base;
 
   const int qi = q0 + wave * 16 + c;
-  float q[DP / 4];
+  float q[DP / 16][4];
 #pragma unroll
-  for (int s = 0; s < DP / 4; ++s) {
-    const int d = 4 * s + g;
-    q[s] = (qi < n && d < D) ? to_f32(Q[(int64_t)qi * p.stride_seq + d]) : 0.f;
-  }
+  for (int j = 0; j < DP / 16; ++j)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int d = 16 * j + 4 * g + t;
+      q[j][t] = (qi < n && d < D) ? to_f32(Q[(int64_t)qi * p.stride_seq + d]) : 0.f;
+    }
   const float qk_scale = p.sm_scale * TM_LOG2E;
   float m_i = TM_NEG_INF, l_i = 0.f;
   f32x4 acc[DP / 16];
@@ -185,24 +206,27 @@ TM_DEV void attn_fwd_generic(const TmAttnFwdArgs &p) {
   if (kbeg < kend) kv.load(K, V, kbeg, n, D, p.stride_seq, tid);
   for (int k0 = kbeg; k0 < kend; k0 += BN) {
     __syncthreads();
-    kv.store(Ks, Vs, tid);
+    kv.store_rows_cols(Ks, Vt, tid);
     __syncthreads();
     if (k0 + BN < kend) kv.load(K, V, k0 + BN, n, D, p.stride_seq, tid);
 
-    float sc[2][4];
+    float sc[KT][4];
     float mx = TM_NEG_INF;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int kt = 0; kt < KT; ++kt) {
       f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int st = 0; st < DP / 4; ++st)
-        s = mfma_f32_16x16x4(Ks[(t * 16 + c) * LD + 4 * st + g], q[st], s);
+      for (int j = 0; j < DP / 16; ++j) {
+        const f32x4 ka = *(const f32x4 *)&Ks[(kt * 16 + c) * LDK + 16 * j + 4 * g];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) s = mfma_f32_16x16x4(ka[t], q[j][t], s);
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int kj = k0 + t * 16 + 4 * g + r;
+        const int kj = k0 + kt * 16 + 4 * g + r;
         float v = s[r] * qk_scale;
         if (kj >= n || (CAUSAL && kj > qi)) v = TM_NEG_INF;
-        sc[t][r] = v;
+        sc[kt][r] = v;
         mx = fmaxf(mx, v);
       }
     }
@@ -214,11 +238,11 @@ TM_DEV void attn_fwd_generic(const TmAttnFwdArgs &p) {
     const float m_use = m_new == TM_NEG_INF ? 0.f : m_new;
     float rs = 0.f;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sc[t][r] = exp2f(sc[t][r] - m_use);
-        rs += sc[t][r];
+        sc[kt][r] = exp2f(sc[kt][r] - m_use);
+        rs += sc[kt][r];
       }
     rs = group4_sum(rs);
     const float alpha = exp2f(m_i - m_use);
@@ -228,11 +252,11 @@ TM_DEV void attn_fwd_generic(const TmAttnFwdArgs &p) {
     for (int dt = 0; dt < DP / 16; ++dt) {
       acc[dt] *= alpha;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int kt = 0; kt < KT; ++kt) {
+        const f32x4 va = *(const f32x4 *)&Vt[(dt * 16 + c) * LDV + kt * 16 + 4 * g];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          acc[dt] = mfma_f32_16x16x4(Vs[(t * 16 + 4 * g + r) * LD + dt * 16 + c],
-                                     round_through<T>(sc[t][r]), acc[dt]);
+        for (int r = 0; r < 4; ++r) acc[dt] = mfma_f32_16x16x4(va[r], round_through<T>(sc[kt][r]), acc[dt]);
+      }
     }
   }
 
