@@ -191,9 +191,10 @@ def _tile_suffix(m, n, cus=256, k=None):
     """The planner's tile choice on an MI355X (256 compute units): rounds of
     resident 256 x 256 tiles (one per CU) at 31 against rounds of 128 x 128
     pairs (two per CU) at 21; with fewer 128 x 128 tiles than CUs, 64 x 64
-    tiles ("_t64").  Given k (whole row-major tiles only), fewer smaller
-    tiles than two per CU and k >= 128 also split the K loop over wave
-    groups ("_k2" for 128 x 128, "_k4" for 64 x 64)."""
+    tiles ("_t64").  Given k >= 128 (whole row-major tiles only), the K loop
+    is split over wave groups: 128 x 128 tiles fewer than two per CU over 2
+    ("_k2"); 64 x 64 tiles over 4 ("_k4") up to one per CU, over 2 ("_k2")
+    up to two."""
     cd = lambda a, b: -(-a // b)
     big = cd(cd(m, 256) * cd(n, 256), cus) * 31 <= cd(cd(m, 128) * cd(n, 128), 2 * cus) * 21
     if big:
@@ -201,14 +202,19 @@ def _tile_suffix(m, n, cus=256, k=None):
     small = cd(m, 128) * cd(n, 128) < cus
     tile = 64 if small else 128
     suffix = "_t64" if small else "_t128"
-    if k is not None and k >= 128 and cd(m, tile) * cd(n, tile) < 2 * cus:
-        suffix += "_k4" if small else "_k2"
+    tiles = cd(m, tile) * cd(n, tile)
+    if k is not None and k >= 128:
+        if small and tiles <= cus:
+            suffix += "_k4"
+        elif small and tiles <= 2 * cus or not small and tiles < 2 * cus:
+            suffix += "_k2"
     return suffix
 @pytest.mark.parametrize("element", ["bf16", "f16"])
 @pytest.mark.parametrize("m,n,k,lda,ldb,ldc,tile", [
     (256, 512, 64, None, None, None, "_t64"),
     (512, 256, 192, None, None, None, "_t64_k4"),   # 3 k-steps over 4 wave groups
     (768, 1024, 320, 328, 1032, 1040, "_t64_k4"),  # padded leading dimensions, 16-byte aligned
+    (256, 8192, 256, None, None, None, "_t64_k2"),  # 512 tiles of 64 x 64: two per CU
     (2048, 2048, 64, None, None, None, "_t128"),
     (2560, 2048, 128, 136, 2056, 2052, "_t128_k2"),
     (2048, 2048, 2048, None, None, None, "_t128_k2"),

@@ -423,10 +423,13 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   extern "C" __global__ __launch_bounds__(TILE * 2) void NAME(TmGemmArgs p) {                 \
     gemm_fast<T, EPI, RAGGED, TILE, TILE, BT, AT>(p);                                          \
   }
-/* whole 128 x 128 (64 x 64) tiles, row-major, the K loop over 2 (4) wave groups */
+/* whole 128 x 128 (64 x 64) tiles, row-major, the K loop over 2 (2 or 4) wave groups */
 #define TM_GEMM_KSPLIT(T, TN)                                                                   \
   extern "C" __global__ __launch_bounds__(512) void tm_gemm_fast_t128_k2_##TN(TmGemmArgs p) {   \
     gemm_fast<T, EPI_NONE, false, 128, 128, false, false, 2>(p);                                \
+  }                                                                                             \
+  extern "C" __global__ __launch_bounds__(256) void tm_gemm_fast_t64_k2_##TN(TmGemmArgs p) {    \
+    gemm_fast<T, EPI_NONE, false, 64, 64, false, false, 2>(p);                                  \
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(512) void tm_gemm_fast_t64_k4_##TN(TmGemmArgs p) {    \
     gemm_fast<T, EPI_NONE, false, 64, 64, false, false, 4>(p);                                  \

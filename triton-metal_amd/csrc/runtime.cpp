@@ -683,14 +683,18 @@ void choose_gemm(Plan &plan, const TmGemmArgs &p, const BuiltinSpec &spec, const
     const bool whole = p.m % tile == 0 && p.n % tile == 0 && p.k % 64 == 0;
     const int64_t tiles = cdiv(p.m, tile) * cdiv(p.n, tile);
     /* whole row-major tiles with fewer 128 x 128 workgroups than two per CU
-     * (one wave per SIMD), or 64 x 64 ones (two waves per CU): the K loop
-     * split over 2 or 4 wave groups inside the workgroup, 512 threads */
-    const bool ksplit = TM_GEMM_KSPLIT && gemm && nn && whole && !big && p.k >= 128 && tiles < 2 * cus;
+     * (one wave per SIMD), or 64 x 64 ones (two waves each): the K loop split
+     * over wave groups inside the workgroup -- 128 x 128 tiles over 2 (512
+     * threads); 64 x 64 tiles over 4 (512 threads, one workgroup per CU) up to
+     * one tile per CU, else over 2 (256 threads, two per CU) up to two */
+    const bool ksplit = TM_GEMM_KSPLIT && gemm && nn && whole && !big && p.k >= 128 &&
+                        (small ? tiles <= 2 * cus : tiles < 2 * cus);
+    const int kg = !ksplit ? 1 : small && tiles > cus ? 2 : small ? 4 : 2;
     plan.variant = format("tm_%s_%s%s%s%s_%s", family, whole ? "fast" : "ragged",
                           nt ? "_nt" : tn ? "_tn" : "", big ? "" : small ? "_t64" : "_t128",
-                          ksplit ? (small ? "_k4" : "_k2") : "", el);
+                          kg == 4 ? "_k4" : kg == 2 ? "_k2" : "", el);
     plan.grid[0] = (unsigned)tiles;
-    plan.block = (unsigned)(ksplit ? 512 : 2 * tile);
+    plan.block = (unsigned)(2 * tile * kg);
   } else {
     plan.variant = format("tm_%s_generic_%s", family, el);
     plan.grid[0] = (unsigned)cdiv(p.m, 64);
