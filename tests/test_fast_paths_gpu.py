@@ -250,7 +250,30 @@ def test_ragged_gemm(element, m, n, k, lda, ldb, ldc, device):
     padding and sentinel rows and columns around C."""
     c, want, variant = _gemm(m, n, k, element, lda, ldb, ldc, poison=True, extra_rows=3)
     tile = _tile_suffix(m, n)
-    assert variant == f"tm_gemm_ragged{tile}_{element}"
+    # the main dispatch (64 x 64 tiles that leave the chip idle run with K
+    # ranges, "_ks", and a reduce dispatch)
+    assert variant.split(" + ")[0] in (f"tm_gemm_ragged{tile}_{element}",
+                                       f"tm_gemm_ragged{tile}_ks_{element}")
+    assert np.all(np.isfinite(c[:m, :n]))
+    assert T.hybrid_error(c[:m, :n], want) <= 2e-2
+    assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)
+
+
+@pytest.mark.parametrize("element", ["bf16", "f16"])
+@pytest.mark.parametrize("m,n,k,lda,ldb,ldc,main,ranges", [
+    (16, 1024, 4096, None, None, None, "tm_gemm_ragged_t64", 16),     # a few rows, long K
+    (64, 2048, 8192, None, None, None, "tm_gemm_fast_t64_k4", 8),     # whole tiles, K groups too
+    (512, 512, 8192, 8200, 520, 516, "tm_gemm_fast_t64_k4", 4),       # padded rows
+    (100, 300, 1000, 1000, 304, 300, "tm_gemm_ragged_t64", 8),        # ragged M, N and K
+    (1, 8, 8192, 8192, 8, 8, "tm_gemm_ragged_t64", 16),               # one row
+])
+def test_gemm_k_ranges(element, m, n, k, lda, ldb, ldc, main, ranges, device):
+    """64 x 64-tile problems with too few tiles to fill the chip split K
+    across workgroups: each range writes an fp32 partial and a reduce
+    dispatch sums them into C (operand padding poisoned, C fenced with
+    sentinels)."""
+    c, want, variant = _gemm(m, n, k, element, lda, ldb, ldc, poison=True, extra_rows=3)
+    assert variant == (f"{main}_ks_{element} + tm_gemm_split_reduce_{element} ({ranges} K ranges)")
     assert np.all(np.isfinite(c[:m, :n]))
     assert T.hybrid_error(c[:m, :n], want) <= 2e-2
     assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)

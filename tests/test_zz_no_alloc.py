@@ -4,7 +4,8 @@ array instead of library-owned memory.  Checked against tm_launch on the same
 inputs, two calls in a row with the second smaller (the array keeps the first
 call's contents, so a missing clear would show), a request larger than the
 array refused before anything runs, a built-in with no work buffer, and the
-generic kernels' range split, whose partials also come from the array."""
+generic kernels' range split and the GEMM's K ranges, whose partials also
+come from the array."""
 
 import ctypes
 import math
@@ -167,3 +168,32 @@ def test_noalloc_range_split_matches_tm_launch_twice(device):
             assert T.hybrid_error(results["tm_launch_noalloc"]["o"], want_o) <= 2e-5
         finally:
             layer.free()
+
+
+def test_noalloc_gemm_k_ranges_match_tm_launch_twice(device):
+    """A GEMM with too few 64 x 64 tiles to fill the chip runs K ranges whose
+    fp32 partials come from the static array: either entry point gives the
+    same bits, two problems in a row with the second smaller."""
+    lib = ops.library("bf16", 64, False)
+    mm = lib.kernels["matmul_kernel"]
+    for m, n, k in ((64, 2048, 8192), (16, 1000, 4096)):
+        print(f"noalloc gemm K ranges m={m} n={n} k={k}", flush=True)
+        rng = np.random.default_rng(m + k)
+        a = DeviceBuffer.from_numpy(round_to(rng.standard_normal((m, k), dtype=np.float32), "bf16"),
+                                    "bfloat16")
+        b = DeviceBuffer.from_numpy(round_to(rng.standard_normal((k, n), dtype=np.float32), "bf16"),
+                                    "bfloat16")
+        c1, c2 = DeviceBuffer((m, n), "bfloat16"), DeviceBuffer((m, n), "bfloat16")
+        try:
+            for entry, c in (("tm_launch", c1), ("tm_launch_noalloc", c2)):
+                c.write(np.full((m, n), 5.0, np.float32))
+                grid, kinds, values = ops.matmul_args(a, b, c, m, n, k)
+                assert _raw_launch(entry, mm, grid, kinds, values) == 0, _core.last_error()
+                assert "K ranges" in _core.kernel_variant(mm), _core.kernel_variant(mm)
+            got, want = c2.float32(), c1.float32()
+            assert np.array_equal(got, want)
+            ref = a.float32().astype(np.float64) @ b.float32().astype(np.float64)
+            assert T.hybrid_error(got, ref) <= 2e-2
+        finally:
+            for x in (a, b, c1, c2):
+                x.free()

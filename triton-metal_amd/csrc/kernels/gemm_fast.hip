@@ -206,8 +206,11 @@ TM_DEV uint32_t g_pack2(float lo, float hi) {
  * accumulators in LDS and group 0 adds them in order and stores.  For grids
  * of about one workgroup per CU (128 x 128 tiles at 2048^3, 64 x 64 at
  * 1024^3), this puts more waves on every SIMD. */
+/* KSPLIT: the K range of the workgroup comes from grid y and p.splits, and
+ * the result is an fp32 partial (64 x 64 tiles only: the instantiations the
+ * planner uses when the tiles alone leave the chip idle). */
 template <typename T, int EPI, bool RAGGED, int BM, int BN, bool BT = false, bool AT = false,
-          int KG = 1>
+          int KG = 1, bool KSPLIT = false>
 TM_DEV void gemm_fast(const TmGemmArgs &p) {
   typedef typename GVec8<T>::type v8;
   constexpr int GBM = BM, GBN = BN;
@@ -280,8 +283,15 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
+  /* this workgroup's k-steps: all of them, or (KSPLIT) the split-th of
+   * p.splits contiguous ranges (grid y) */
+  static_assert(!KSPLIT || (BM == 64 && EPI == EPI_NONE), "K ranges: 64 x 64 GEMM tiles");
   const int ksteps = (p.k + GBK - 1) / GBK;
-  if (kgrp < ksteps) stage(lds_a0, lds_b0, kgrp);
+  const int splits = KSPLIT && p.splits > 1 ? p.splits : 1;
+  const int split = splits > 1 ? (int)blockIdx.y : 0;
+  const int kbeg = splits > 1 ? (int)((unsigned)(split * ksteps) / (unsigned)splits) : 0;
+  const int kend = splits > 1 ? (int)((unsigned)((split + 1) * ksteps) / (unsigned)splits) : ksteps;
+  if (kbeg + kgrp < kend) stage(lds_a0, lds_b0, kbeg + kgrp);
   g_wait_vmem();
   __syncthreads();
 
@@ -290,10 +300,10 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
    * the range check. */
   auto step = [&](auto last_tag, const char *ca, const char *cb, char *na, char *nb, int kb) {
     constexpr bool LAST = decltype(last_tag)::value;
-    if (!LAST && kb + KG < ksteps) stage(na, nb, kb + KG);
+    if (!LAST && kb + KG < kend) stage(na, nb, kb + KG);
     /* a group with no k-step left in the last round still meets its barrier */
 #pragma unroll
-    for (int ks = 0; ks < 2 && (KG == 1 || kb < ksteps); ++ks) {
+    for (int ks = 0; ks < 2 && (KG == 1 || kb < kend); ++ks) {
       v8 bf[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -331,22 +341,22 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   using Full = std::integral_constant<bool, false>;
   using Last = std::integral_constant<bool, true>;
 
-  /* with a ragged K the last step runs masked */
-  const int kfull = RAGGED && p.k % GBK ? ksteps - 1 : ksteps;
+  /* with a ragged K the last step (in the last range) runs masked */
+  const int kfull = RAGGED && p.k % GBK && kend == ksteps ? kend - 1 : kend;
   if constexpr (KG == 1) {
-    for (int kb = 0; kb < kfull; kb += 2) {
+    for (int kb = kbeg; kb < kfull; kb += 2) {
       step(Full{}, lds_a0, lds_b0, lds_a1, lds_b1, kb);
       if (kb + 1 < kfull) step(Full{}, lds_a1, lds_b1, lds_a0, lds_b0, kb + 1);
     }
-    if (RAGGED && kfull < ksteps) {
-      const bool odd = kfull & 1;
+    if (RAGGED && kfull < kend) {
+      const bool odd = (kfull - kbeg) & 1;
       step(Last{}, odd ? lds_a1 : lds_a0, odd ? lds_b1 : lds_b0, nullptr, nullptr, kfull);
     }
   } else {
-    const int rounds = (ksteps + KG - 1) / KG;
+    const int rounds = (kend - kbeg + KG - 1) / KG;
     for (int r = 0; r < rounds; r += 2) {
-      step(Full{}, lds_a0, lds_b0, lds_a1, lds_b1, r * KG + kgrp);
-      if (r + 1 < rounds) step(Full{}, lds_a1, lds_b1, lds_a0, lds_b0, (r + 1) * KG + kgrp);
+      step(Full{}, lds_a0, lds_b0, lds_a1, lds_b1, kbeg + r * KG + kgrp);
+      if (r + 1 < rounds) step(Full{}, lds_a1, lds_b1, lds_a0, lds_b0, kbeg + (r + 1) * KG + kgrp);
     }
     /* groups 1 .. KG-1 leave their partial C^T tiles in their own LDS (the
      * last barrier above ended every read of it); group 0 adds them */
@@ -371,6 +381,23 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
 
   /* acc[i][j] is the C^T tile: lane holds row m0 + wm*BM/2 + i*16 + c,
    * columns n0 + wn*64 + j*16 + 4g .. +3 */
+  if constexpr (EPI == EPI_NONE) {
+    if (splits > 1) {
+      /* this range's fp32 partial: rows of round4(n) floats */
+      const int64_t np = (p.n + 3) & ~3;
+      float *part = p.part + (int64_t)split * p.m * np;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int m = m0 + wm * (BM / 2) + i * 16 + c;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int n = n0 + wn * 64 + j * 16 + 4 * g;
+          if (m < p.m && n < p.n) *(f32x4 *)(part + m * np + n) = acc[i][j];
+        }
+      }
+      return;
+    }
+  }
   /* The bias of the wave's 16 columns, loaded once before any store (the
    * compiler cannot move the loads across stores to C that might alias). */
   float bias[4][4];
@@ -419,10 +446,55 @@ TM_DEV void gemm_fast(const TmGemmArgs &p) {
   }
 }
 
+/* The K ranges' partials summed in range order (deterministic) into C in the
+ * element type: one thread per four columns of a row. */
+template <typename T>
+TM_DEV void gemm_split_reduce(const TmGemmArgs &p) {
+  const int64_t np4 = (p.n + 3) >> 2;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)p.m * np4) return;
+  const int64_t m = idx / np4;
+  const int n = (int)(idx - m * np4) * 4;
+  const int64_t plane = (int64_t)p.m * np4 * 4;
+  f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < p.splits; ++s) sum += *(const f32x4 *)(p.part + s * plane + m * np4 * 4 + n);
+  T *dst = (T *)p.c + m * p.scm + n;
+  if (n + 4 <= p.n) {
+    u32x2 w;
+    w[0] = g_pack2<T>(sum[0], sum[1]);
+    w[1] = g_pack2<T>(sum[2], sum[3]);
+    *(u32x2 *)dst = w;
+  } else {
+    for (int r = 0; n + r < p.n; ++r) dst[r] = (T)sum[r];
+  }
+}
+extern "C" __global__ __launch_bounds__(256) void tm_gemm_split_reduce_bf16(TmGemmArgs p) {
+  gemm_split_reduce<bf16_t>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void tm_gemm_split_reduce_f16(TmGemmArgs p) {
+  gemm_split_reduce<f16_t>(p);
+}
+
 #define TM_GEMM_ONE(NAME, T, EPI, RAGGED, TILE, BT, AT)                                     \
   extern "C" __global__ __launch_bounds__(TILE * 2) void NAME(TmGemmArgs p) {                 \
     gemm_fast<T, EPI, RAGGED, TILE, TILE, BT, AT>(p);                                          \
   }
+/* the 64 x 64-tile GEMMs with K ranges across workgroups ("_ks") */
+#define TM_GEMM_KS(NAME, T, RAGGED, BT, AT, KG)                                               \
+  extern "C" __global__ __launch_bounds__(128 * KG) void NAME(TmGemmArgs p) {                 \
+    gemm_fast<T, EPI_NONE, RAGGED, 64, 64, BT, AT, KG, true>(p);                               \
+  }
+#define TM_GEMM_KS_ALL(T, TN)                                                  \
+  TM_GEMM_KS(tm_gemm_fast_t64_ks_##TN, T, false, false, false, 1)              \
+  TM_GEMM_KS(tm_gemm_ragged_t64_ks_##TN, T, true, false, false, 1)             \
+  TM_GEMM_KS(tm_gemm_fast_nt_t64_ks_##TN, T, false, true, false, 1)            \
+  TM_GEMM_KS(tm_gemm_ragged_nt_t64_ks_##TN, T, true, true, false, 1)           \
+  TM_GEMM_KS(tm_gemm_fast_tn_t64_ks_##TN, T, false, false, true, 1)            \
+  TM_GEMM_KS(tm_gemm_ragged_tn_t64_ks_##TN, T, true, false, true, 1)           \
+  TM_GEMM_KS(tm_gemm_fast_t64_k2_ks_##TN, T, false, false, false, 2)           \
+  TM_GEMM_KS(tm_gemm_fast_t64_k4_ks_##TN, T, false, false, false, 4)
+TM_GEMM_KS_ALL(bf16_t, bf16)
+TM_GEMM_KS_ALL(f16_t, f16)
 /* whole 128 x 128 (64 x 64) tiles, row-major, the K loop over 2 (2 or 4) wave groups */
 #define TM_GEMM_KSPLIT(T, TN)                                                                   \
   extern "C" __global__ __launch_bounds__(512) void tm_gemm_fast_t128_k2_##TN(TmGemmArgs p) {   \

@@ -603,6 +603,11 @@ void validate_attn_common(const char *name, int64_t heads, int32_t stride_head,
   if (heads > 65535) throw TmError(format("%s: %lld heads exceeds 65535", name, (long long)heads));
 }
 
+/* 0 turns the bf16/f16 GEMM's K split across workgroups off (measurement builds) */
+#ifndef TM_GEMM_SPLITK
+#define TM_GEMM_SPLITK 1
+#endif
+
 /* 0 turns the bf16/f16 GEMM's intra-workgroup K split off (measurement builds) */
 #ifndef TM_GEMM_KSPLIT
 #define TM_GEMM_KSPLIT 1
@@ -773,6 +778,51 @@ void *plan_workspace(const Library &lib, size_t need, const Scratch *scratch) {
   return lib.workspace;
 }
 
+/* bf16/f16 GEMMs on 64 x 64 tiles with too few tiles to fill the chip (a
+ * few rows against a large N K, or a small M N with a long K): the K loop
+ * split across workgroups into `splits` ranges (grid y), each writing an fp32
+ * partial product, then a reduce dispatch that sums them in range order into
+ * C.  Target: about four 2-wave workgroups per CU (one 8-wave K-group
+ * workgroup), at least two k-steps per wave group and range.  Returns false
+ * (plan untouched) when the split does not apply or no work memory is
+ * available. */
+bool plan_gemm_split(Plan &plan, TmGemmArgs &p, const BuiltinSpec &spec, const Library &lib,
+                     const Scratch *scratch) {
+  /* the split is compiled into "_ks" instantiations of the 64 x 64-tile
+   * GEMM kernels only */
+  if (!TM_GEMM_SPLITK || spec.element == Element::F32 || plan.variant.find("_t64") == std::string::npos ||
+      plan.variant.rfind("tm_gemm_", 0) != 0)
+    return false;
+  const int64_t cus = std::max(device().compute_units, 1);
+  const int64_t tiles = plan.grid[0];
+  const int64_t kg = plan.block / 128; /* wave groups of the K split inside the workgroup */
+  const int64_t ksteps = cdiv(p.k, 64);
+  const int64_t target = (kg == 1 ? 4 : 1) * cus;
+  const int64_t splits = std::min<int64_t>({target / std::max<int64_t>(tiles, 1), ksteps / (2 * kg), 16});
+  if (splits < 2) return false;
+  const int64_t np = (p.n + 3) & ~int64_t(3);
+  void *work = plan_workspace(lib, (size_t)splits * (size_t)p.m * (size_t)np * 4, scratch);
+  if (!work) return false;
+  p.part = (float *)work;
+  p.splits = (int32_t)splits;
+  Plan main = plan, reduce;
+  /* the "_ks" instantiation of the planned kernel */
+  const std::string suffix = std::string("_") + element_name(spec.element);
+  main.variant = plan.variant.substr(0, plan.variant.size() - suffix.size()) + "_ks" + suffix;
+  main.grid[1] = (unsigned)splits;
+  set_kernarg(main, p);
+  reduce.variant = format("tm_gemm_split_reduce_%s", element_name(spec.element));
+  reduce.grid[0] = (unsigned)cdiv((int64_t)p.m * (np / 4), 256);
+  reduce.block = 256;
+  set_kernarg(reduce, p);
+  for (Plan *part : {&main, &reduce}) part->function = builtin_function(part->variant);
+  plan.function = main.function;
+  plan.variant = format("%s + %s (%d K ranges)", main.variant.c_str(), reduce.variant.c_str(),
+                        (int)splits);
+  plan.sequence = {main, reduce};
+  return true;
+}
+
 /* attn_bwd_fused under bwd=stash as two dispatches: the dK/dV kernel, which
  * also writes dS^T into `stash`, then the dQ kernel that reads it.  Every
  * stash element the dQ kernel reads for a stored query is written first (the
@@ -895,6 +945,7 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
         return plan;
       }
       choose_gemm(plan, p, spec, "gemm");
+      if (plan_gemm_split(plan, p, spec, lib, scratch)) return plan;
       set_kernarg(plan, p);
       break;
     }

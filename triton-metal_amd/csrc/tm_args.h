@@ -25,6 +25,10 @@ struct TmGemmArgs {
   int32_t m, n, k;
   int32_t sam, sak, sbk, sbn, scm, scn;
   const void *bias; /* [n] elements; read only by the bias + ReLU epilogue kernels */
+  /* K split across workgroups (splits > 1, grid y): fp32 partial products
+   * [splits][m][round4(n)], summed into c by the reduce dispatch */
+  float *part;
+  int32_t splits;
 };
 
 struct TmAttnFwdArgs {
