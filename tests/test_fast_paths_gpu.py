@@ -382,6 +382,35 @@ def _random_gemm_cases(count=36, seed=123):
     return [(m, n, k, layout, pad(k), pad(n), pad(m), el) for m, n, k, layout, pad, el in cases]
 
 
+def _random_k_range_cases(count=18, seed=7):
+    """Seeded shapes that take K ranges: M and N up to 300 (few 64 x 64
+    tiles), K from 1000 to 6000, every layout, padded leading dimensions."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        m, n = (int(x) for x in rng.integers(1, 300, 2))
+        k = int(rng.integers(1000, 6000))
+        pad = lambda x: -(-(x + int(rng.integers(0, 17))) // 8) * 8
+        out.append((m, n, k, ("nn", "nt", "tn")[i % 3], pad(k), pad(n), pad(m), ("bf16", "f16")[i % 2]))
+    return out
+
+
+@pytest.mark.parametrize("m,n,k,layout,pk,pn,pm,element", _random_k_range_cases())
+def test_gemm_k_range_sweep(m, n, k, layout, pk, pn, pm, element, device):
+    """Seeded small-M-N, long-K shapes: every one runs K ranges across
+    workgroups and a reduce, against fp64 with inf/NaN in the padding."""
+    if layout == "nn":
+        c, want, variant = _gemm(m, n, k, element, pk, pn, pn, poison=True, extra_rows=3)
+    elif layout == "nt":
+        c, want, variant = _gemm_nt(m, n, k, element, pk, pk, pn)
+    else:
+        c, want, variant = _gemm_tn(m, n, k, element, pm, pn, pn)
+    assert "_ks_" in variant and "K ranges" in variant, variant
+    assert np.all(np.isfinite(c[:m, :n]))
+    assert T.hybrid_error(c[:m, :n], want) <= 2e-2
+    assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)
+
+
 @pytest.mark.parametrize("m,n,k,layout,pk,pn,pm,element", _random_gemm_cases())
 def test_gemm_layout_sweep(m, n, k, layout, pk, pn, pm, element, device):
     """Seeded random shapes and layouts through the specialised kernels,
