@@ -113,23 +113,51 @@ TM_DEV void gemm_generic(const TmGemmArgs &p) {
 template <typename T, int ROWS, int DP>
 struct TileStager {
   static constexpr int PER = ROWS * DP / 256;
-  static_assert(ROWS * DP % 256 == 0, "whole elements per thread");
+  static_assert(ROWS * DP % 1024 == 0, "four consecutive elements per thread");
+  /* DP <= 64: a thread's elements come in runs of four consecutive ones,
+   * e = 4 (tid + 256 (i / 4)) + i % 4, loaded together when they can be
+   * (measured: fp32 D = 64 backward 5% faster; at DP = 128 the forward ran
+   * 11% slower, so wider tiles keep e = tid + 256 i, one load each) */
+  static constexpr bool RUNS = DP <= 64;
   float ra[PER], rb[PER];
+  static TM_DEV int elem(int tid, int i) { return RUNS ? 4 * (tid + 256 * (i / 4)) + i % 4 : tid + 256 * i; }
+  /* RUNS, with D and the row stride multiples of 4 and both bases aligned:
+   * one 16-byte (f32) or 8-byte load per run; else one load per element */
   TM_DEV void load(const T *a, const T *b, int r0, int n, int D, int64_t ss, int tid) {
+    const bool vec = RUNS && D % 4 == 0 && ss % 4 == 0 &&
+                     ((uintptr_t)a | (uintptr_t)b) % (4 * sizeof(T)) == 0;
+    if (vec) {
+      typedef T t4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int e = tid + 256 * i;
-      const int r = r0 + e / DP, cc = e % DP;
-      const bool ok = r < n && cc < D;
-      const int64_t off = (int64_t)r * ss + cc;
-      ra[i] = ok ? to_f32(a[off]) : 0.f;
-      rb[i] = ok ? to_f32(b[off]) : 0.f;
+      for (int i = 0; i < PER; i += 4) {
+        const int e = elem(tid, i);
+        const int r = r0 + e / DP, cc = e % DP;
+        const bool ok = r < n && cc < D;
+        const int64_t off = (int64_t)r * ss + cc;
+        const t4 x = ok ? *(const t4 *)(a + off) : (t4){};
+        const t4 y = ok ? *(const t4 *)(b + off) : (t4){};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          ra[i + j] = to_f32(x[j]);
+          rb[i + j] = to_f32(y[j]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int e = elem(tid, i);
+        const int r = r0 + e / DP, cc = e % DP;
+        const bool ok = r < n && cc < D;
+        const int64_t off = (int64_t)r * ss + cc;
+        ra[i] = ok ? to_f32(a[off]) : 0.f;
+        rb[i] = ok ? to_f32(b[off]) : 0.f;
+      }
     }
   }
   TM_DEV void store(float *as, float *bs, int tid) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int e = tid + 256 * i;
+      const int e = elem(tid, i);
       as[(e / DP) * (DP + 1) + e % DP] = ra[i];
       bs[(e / DP) * (DP + 1) + e % DP] = rb[i];
     }
@@ -140,7 +168,7 @@ struct TileStager {
   TM_DEV void store_rows_cols(float *as, float *bt, int tid) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int e = tid + 256 * i;
+      const int e = elem(tid, i);
       as[(e / DP) * (DP + 4) + e % DP] = ra[i];
       bt[(e % DP) * (ROWS + 4) + e / DP] = rb[i];
     }
