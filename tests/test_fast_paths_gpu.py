@@ -279,6 +279,36 @@ def test_gemm_k_ranges(element, m, n, k, lda, ldb, ldc, main, ranges, device):
     assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)
 
 
+def test_gemm_k_ranges_queued_back_to_back(device):
+    """Three K-range GEMMs queued without waiting, each needing more work
+    memory than the last (the library grows its workspace between them, after
+    the queued dispatches drain), then one synchronize: every result is
+    right."""
+    kern = ops.library("bf16").kernels["matmul_kernel"]
+    rng = np.random.default_rng(11)
+    shapes = ((16, 256, 4096), (64, 1024, 4096), (200, 2000, 3000))
+    bufs, wants = [], []
+    try:
+        for m, n, k in shapes:
+            a = round_to(rng.standard_normal((m, k), dtype=np.float32), "bf16")
+            b = round_to(rng.standard_normal((k, n), dtype=np.float32), "bf16")
+            A, B = DeviceBuffer.from_numpy(a, "bfloat16"), DeviceBuffer.from_numpy(b, "bfloat16")
+            C = DeviceBuffer.from_numpy(np.full((m, n), -7.0, np.float32), "bfloat16")
+            bufs.append((A, B, C))
+            wants.append(a.astype(np.float64) @ b.astype(np.float64))
+        for (m, n, k), (A, B, C) in zip(shapes, bufs):
+            grid, kinds, values = ops.matmul_args(A, B, C, m, n, k)
+            _core.launch_async(kern, grid, 128, kinds, values)
+            assert "K ranges" in _core.kernel_variant(kern), _core.kernel_variant(kern)
+        _core.synchronize()
+        for (A, B, C), want in zip(bufs, wants):
+            assert T.hybrid_error(C.float32(), want) <= 2e-2
+    finally:
+        for trio in bufs:
+            for x in trio:
+                x.free()
+
+
 def _gemm_nt(m, n, k, element, lda=None, ldbt=None, ldc=None, seed=0):
     """C = A B with B stored transposed (bt[n, k], row stride ldbt: the
     x @ W^T layout); the padding columns of A and of B^T hold inf, and C is
