@@ -266,6 +266,8 @@ def test_ragged_gemm(element, m, n, k, lda, ldb, ldc, device):
     (512, 512, 8192, 8200, 520, 516, "tm_gemm_fast_t64_k4", 4),       # padded rows
     (100, 300, 1000, 1000, 304, 300, "tm_gemm_ragged_t64", 8),        # ragged M, N and K
     (1, 8, 8192, 8192, 8, 8, "tm_gemm_ragged_t64", 16),               # one row
+    (64, 64, 65536, None, None, None, "tm_gemm_fast_t64_k4", 16),     # one tile, K of 1024 steps
+    (1, 1, 65536, 65536, 8, 4, "tm_gemm_ragged_t64", 16),             # one element, long K
 ])
 def test_gemm_k_ranges(element, m, n, k, lda, ldb, ldc, main, ranges, device):
     """64 x 64-tile problems with too few tiles to fill the chip split K
