@@ -1423,16 +1423,243 @@ TM_DEV void attn_dq_stash(const TmAttnFusedArgs &a) {
   }
 }
 
+/* ---- backward: dK, dV at two waves per SIMD -------------------------------
+ * The same work split as attn_dkdv_fast (a workgroup of 4 waves owns 128 keys,
+ * a wave 32 of them, and walks 32-query blocks), built for two waves per SIMD
+ * so that the other workgroup's wave fills the MFMA pipe while this one runs
+ * its softmax.  To fit 256 registers the wave keeps only K^T in registers;
+ * the workgroup's 128 V rows are copied to LDS once and read per block.
+ * Q/dO tiles are double-buffered.  LDS is addressed by 32-bit offsets whose
+ * lane parts are computed once (row offsets within a tile are immediates).
+ * Scheduling fences sit only between the three phases of a block (score
+ * MFMAs, softmax, gradient MFMAs): without them the compiler hoists the whole
+ * block's operand reads and spills; finer fences (per k-step or per two d
+ * tiles) measured 2-3% slower.  The masked and the interior blocks run in
+ * separate loops: a branch between the two forms inside one loop body made
+ * the register allocator spill the accumulators.
+ * As in attn_dkdv_fast, the dP MFMAs run on -V (negated once in LDS) and
+ * start from Delta, so they deliver Delta - dP, and the kernel carries
+ * -dS = P (Delta - dP) with one multiply; the arithmetic is the same as that
+ * kernel's (and its fused and stash forms'), so dK and dV are bit-identical. */
+template <typename T, int D, bool CAUSAL>
+TM_DEV void attn_dkdv_2w(const TmAttnDkdvArgs &p) {
+  static_assert(D == 128, "two-wave dK/dV is built for head_dim 128");
+  constexpr int BN = 128, KW = 32, BM = 32;
+  constexpr int KS = D / 32, DT = D / 16;
+  constexpr int TILE = BM * D * 2;
+  constexpr int VT = BN * D * 2;
+  constexpr int STATS = 2 * TILE;
+  constexpr int BUF = 2 * TILE + BM * 8;
+  __shared__ __align__(1024) char lds[VT + 2 * BUF];
+  const uint32_t vbase = lds_addr(lds), buf0 = vbase + VT, buf1 = buf0 + BUF;
+
+  typedef typename Vec8<T>::type v8;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const int n = p.n_ctx;
+  const int nkb = (n + BN - 1) / BN;
+  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  int bh, kb;
+  if (CAUSAL) {
+    causal_order(logical, nkb, p.heads, bh, kb);
+  } else {
+    bh = logical / nkb;
+    kb = logical - bh * nkb;
+  }
+  const int k0 = kb * BN;
+  const int kw0 = k0 + wave * KW;
+  const int64_t base = (int64_t)bh * p.stride_head;
+  const int64_t ss = p.stride_seq;
+  const T *Qg = (const T *)p.q + base;
+  const T *Kg = (const T *)p.k + base;
+  const T *Vg = (const T *)p.v + base;
+  const T *dOg = (const T *)p.dout + base;
+  T *dKg = (T *)p.dk + base;
+  T *dVg = (T *)p.dv + base;
+  const float *Lg = p.lse + (int64_t)bh * p.stride_lse;
+  const float *Dg = p.delta + (int64_t)bh * p.stride_lse;
+
+  const int q_start = CAUSAL ? k0 : 0;
+  const int nblocks = (n - q_start + BM - 1) / BM;
+
+  TileCopy<T, D, BM, KEY_BOTH> qcp;  /* Q and dO rows share the lane offsets */
+  TileCopy<T, D, BN, KEY_B128> vcp;
+  qcp.init(ss, wave, lane);
+  vcp.init(ss, wave, lane);
+  auto stage = [&](uint32_t buf, int blk) {
+    const int qs = q_start + blk * BM;
+    qcp.copy(Qg, ss, qs, n, buf, wave);
+    qcp.copy(dOg, ss, qs, n, buf + TILE, wave);
+    if (wave == 0) {
+      const int q = min(qs + (lane & 31), n - 1);
+      lds_copy4_global(lane < 32 ? Lg + q : Dg + q, buf + STATS);
+    }
+  };
+  vcp.copy(Vg, ss, k0, n, vbase, wave);
+  if (nblocks > 0) stage(buf0, 0);
+
+  u32x4 kf[2][KS];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    const int key = min(kw0 + kt * 16 + c, n - 1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      kf[kt][ks] = *(const u32x4 *)(Kg + (int64_t)key * ss + ks * 32 + 8 * g);
+  }
+  /* lane parts of the operand offsets: rows c (+16 qt or kt immediates) at
+   * chunk 4 ks + g of a KEY_BOTH tile (Q, dO) or a KEY_B128 tile (V); and the
+   * k-major reads of d tile dt (rows 4g + c/4, +16 immediate) */
+  uint32_t qoff[KS], voff[KS], kmoff[DT];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    qoff[ks] = (uint32_t)tile_off<D>(c, ks * 4 + g);
+    voff[ks] = (uint32_t)tile_off<D, KEY_B128>(c, ks * 4 + g) + (uint32_t)(wave * KW * D * 2);
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+    kmoff[dt] = (uint32_t)(tile_off<D>(4 * g + (c >> 2), 2 * dt + ((c & 3) >> 1)) + ((c & 1) << 3));
+  const float qk_scale = p.sm_scale * TM_LOG2E;
+  f32x4 dk[DT][2], dv[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+    dk[dt][0] = dk[dt][1] = dv[dt][0] = dv[dt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  auto block = [&](auto edge_tag, uint32_t cur, int blk) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    const int qs = q_start + blk * BM;
+    f32x4 s[2][2], dp[2][2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const f32x4 dl = __builtin_bit_cast(f32x4, lds_read16(cur + STATS + 128 + (qt * 16 + 4 * g) * 4));
+      s[0][qt] = s[1][qt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      dp[0][qt] = dp[1][qt] = dl;
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const v8 qa = as_vec8<T>(lds_read16(cur + qoff[ks] + qt * 16 * D * 2));
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) s[kt][qt] = mfma_16x16x32(qa, as_vec8<T>(kf[kt][ks]), s[kt][qt]);
+      }
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const v8 vb = as_vec8<T>(lds_read16(vbase + voff[ks] + kt * 16 * D * 2));
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+          const v8 da = as_vec8<T>(lds_read16(cur + TILE + qoff[ks] + qt * 16 * D * 2));
+          dp[kt][qt] = mfma_16x16x32(da, vb, dp[kt][qt]);
+        }
+      }
+    }
+    TM_FENCE();
+    u32x4 pf[2], dsf[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int key = kw0 + kt * 16 + c;
+      float pr[2][4], ds[2][4];
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const f32x4 lse = __builtin_bit_cast(f32x4, lds_read16(cur + STATS + (qt * 16 + 4 * g) * 4));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float x = __builtin_fmaf(s[kt][qt][r], qk_scale, -lse[r]);
+          if (EDGE) {
+            const int qi = qs + qt * 16 + 4 * g + r;
+            x = (qi >= n || (CAUSAL && qi < key)) ? TM_NEG_INF : x;
+          }
+          pr[qt][r] = fast_exp2(x);
+          ds[qt][r] = pr[qt][r] * dp[kt][qt][r]; /* -dS */
+        }
+      }
+      pf[kt] = (u32x4){pack2<T>(pr[0][0], pr[0][1]), pack2<T>(pr[0][2], pr[0][3]),
+                       pack2<T>(pr[1][0], pr[1][1]), pack2<T>(pr[1][2], pr[1][3])};
+      dsf[kt] = (u32x4){pack2<T>(ds[0][0], ds[0][1]), pack2<T>(ds[0][2], ds[0][3]),
+                        pack2<T>(ds[1][0], ds[1][1]), pack2<T>(ds[1][2], ds[1][3])};
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const v8 doa = as_vec8<T>(lds_read_kmajor(cur + TILE + kmoff[dt], 0, 16 * D * 2));
+      const v8 qa = as_vec8<T>(lds_read_kmajor(cur + kmoff[dt], 0, 16 * D * 2));
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        dv[dt][kt] = mfma_16x16x32(doa, as_vec8<T>(pf[kt]), dv[dt][kt]);
+        dk[dt][kt] = mfma_16x16x32(qa, as_vec8<T>(dsf[kt]), dk[dt][kt]);
+      }
+    }
+    TM_FENCE();
+  };
+  using Interior = std::integral_constant<bool, false>;
+  using Edge = std::integral_constant<bool, true>;
+
+  wait_vmem();
+  __syncthreads();
+  /* -V in LDS: every sign bit flipped once (exact) */
+#pragma unroll
+  for (int e = 0; e < VT / (256 * 16); ++e) {
+    const uint32_t a = vbase + (uint32_t)(e * 256 + tid) * 16;
+    const u32x4 x = lds_read16(a) ^ (u32x4){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+    *(__attribute__((address_space(3))) u32x4 *)(lds_char_t *)(uintptr_t)a = x;
+  }
+  __syncthreads();
+  const int band = CAUSAL ? BN / BM : 0;
+  const int full = (n - q_start) / BM;
+  /* block i reads buffer i mod 2 while block i+1 is copied into the other;
+   * the masked blocks (the diagonal band, a ragged end) and the interior run
+   * in loops of their own */
+  auto step = [&](auto edge_tag, int i) {
+    const uint32_t cur = (i & 1) ? buf1 : buf0, nxt = (i & 1) ? buf0 : buf1;
+    if (i + 1 < nblocks) stage(nxt, i + 1);
+    block(edge_tag, cur, i);
+    wait_vmem();
+    __syncthreads();
+  };
+  const int interior_end = min(full, nblocks);
+  int i = 0;
+  for (; i < nblocks && i < band; ++i) step(Edge{}, i);
+  for (; i < interior_end; ++i) step(Interior{}, i);
+  for (; i < nblocks; ++i) step(Edge{}, i);
+
+  const float dk_scale = -p.sm_scale; /* dk holds -dK / sm_scale */
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    const int key = kw0 + kt * 16 + c;
+    if (key < n) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        u32x2 wk, wv;
+        wk[0] = pack2<T>(dk[dt][kt][0] * dk_scale, dk[dt][kt][1] * dk_scale);
+        wk[1] = pack2<T>(dk[dt][kt][2] * dk_scale, dk[dt][kt][3] * dk_scale);
+        wv[0] = pack2<T>(dv[dt][kt][0], dv[dt][kt][1]);
+        wv[1] = pack2<T>(dv[dt][kt][2], dv[dt][kt][3]);
+        *(u32x2 *)(dKg + (int64_t)key * ss + dt * 16 + 4 * g) = wk;
+        *(u32x2 *)(dVg + (int64_t)key * ss + dt * 16 + 4 * g) = wv;
+      }
+    }
+  }
+}
+
+
 #define TM_BWD_FAST(T, TN, D, CAUSAL, CN)                                                     \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void  \
   tm_attn_dq_fast_##TN##_d##D##CN(TmAttnDqArgs p) {                                           \
     attn_dq_fast<T, D, CAUSAL>(p);                                                            \
   }                                                                                           \
-  /* dK, dV accumulators (128 registers) plus the wave's K^T and V^T fragments do   \
-   * not fit in 256 registers: one wave per SIMD, accumulators in AGPRs. */               \
-  extern "C" __global__ __launch_bounds__(256) void tm_attn_dkdv_fast_##TN##_d##D##CN(        \
+  TM_DKDV_FAST_##D(T, TN, CAUSAL, CN)
+/* head_dim 128: the two-waves-per-SIMD kernel (0.99-1.03 ms at B4 H32 S4096
+ * causal against 1.11-1.16 ms for attn_dkdv_fast at one wave per SIMD, whose
+ * dK, dV accumulators plus K^T and V^T fragments need more than 256
+ * registers); head_dim 64: attn_dkdv_fast, one wave per SIMD */
+#define TM_DKDV_FAST_128(T, TN, CAUSAL, CN)                                                   \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void  \
+  tm_attn_dkdv_fast_##TN##_d128##CN(TmAttnDkdvArgs p) {                                       \
+    attn_dkdv_2w<T, 128, CAUSAL>(p);                                                          \
+  }
+#define TM_DKDV_FAST_64(T, TN, CAUSAL, CN)                                                    \
+  extern "C" __global__ __launch_bounds__(256) void tm_attn_dkdv_fast_##TN##_d64##CN(         \
       TmAttnDkdvArgs p) {                                                                     \
-    attn_dkdv_fast<T, D, CAUSAL>(p);                                                          \
+    attn_dkdv_fast<T, 64, CAUSAL>(p);                                                         \
   }
 /* Single-pass backward with atomic dQ (opt-in: bwd=atomic): the dK/dV
  * kernel plus dQ = dS K per query block, and the passes around it. */
