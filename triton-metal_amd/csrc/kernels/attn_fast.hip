@@ -688,14 +688,17 @@ TM_PRE_FAST(f16_t, f16, 128)
  * dS is rounded to the element type before its dot, as the reference does
  * (AttentionBackwardKernel.swift:155-160).  The dP^T MFMAs start from -Delta
  * (a lane's four values share its query) instead of zero, so they deliver
- * dP^T - Delta with no subtraction per element. */
+ * dP^T - Delta with no subtraction per element.  LDS is addressed by 32-bit
+ * offsets whose lane parts are computed once: with flat tile pointers (and a
+ * branch between the two buffer phases in the masked loop) the kernel needed
+ * 256 registers and spilled; so it needs 234 and runs 3% faster. */
 template <typename T, int D, bool CAUSAL>
 TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
   constexpr int BM = 128, BN = 64, QW = 32;
   constexpr int KS = D / 32;
   constexpr int TILE = BN * D * 2;
-  __shared__ __align__(1024) char lds_a[2 * TILE];
-  __shared__ __align__(1024) char lds_b[2 * TILE];
+  __shared__ __align__(1024) char lds[4 * TILE];
+  const uint32_t buf_a = lds_addr(lds), buf_b = buf_a + 2 * TILE;
 
   typedef typename Vec8<T>::type v8;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -726,10 +729,19 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
 
   const int kend = CAUSAL ? min(n, q0 + BM) : n;
   const int nblocks = (kend + BN - 1) / BN;
+  TileCopy<T, D, BN, KEY_BOTH> kvcp; /* K and V rows share the lane offsets */
+  kvcp.init(ss, wave, lane);
   if (nblocks > 0) {
-    stage_rows<T, D, BN>(Kg, ss, 0, n, lds_a, wave, lane);
-    stage_rows<T, D, BN>(Vg, ss, 0, n, lds_a + TILE, wave, lane);
+    kvcp.copy(Kg, ss, 0, n, buf_a, wave);
+    kvcp.copy(Vg, ss, 0, n, buf_a + TILE, wave);
   }
+  /* lane parts of the operand offsets (row offsets of kt are immediates) */
+  uint32_t koff[KS], kmoff[D / 16];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = (uint32_t)tile_off<D>(c, ks * 4 + g);
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt)
+    kmoff[dt] = (uint32_t)(tile_off<D>(4 * g + (c >> 2), 2 * dt + ((c & 3) >> 1)) + ((c & 1) << 3));
 
   u32x4 qf[2][KS], df[2][KS];
   float lse[2], dlt[2];
@@ -754,12 +766,12 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
   wait_vmem();
   __syncthreads();
 
-  auto step = [&](auto edge_tag, const char *cur, char *nxt, int j) {
+  auto step = [&](auto edge_tag, uint32_t cur, uint32_t nxt, int j) {
     constexpr bool EDGE = decltype(edge_tag)::value;
     const int k0 = j * BN;
     if (j + 1 < nblocks) {
-      stage_rows<T, D, BN>(Kg, ss, k0 + BN, n, nxt, wave, lane);
-      stage_rows<T, D, BN>(Vg, ss, k0 + BN, n, nxt + TILE, wave, lane);
+      kvcp.copy(Kg, ss, k0 + BN, n, nxt, wave);
+      kvcp.copy(Vg, ss, k0 + BN, n, nxt + TILE, wave);
     }
     /* two 32-key halves: scores, dS, then the dQ MFMAs of that half, so only
      * half of S^T and dP^T is live at a time */
@@ -774,9 +786,8 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
         dp[h][1] = ndlt[1];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          const v8 ka = as_vec8<T>(*(const u32x4 *)(cur + tile_off<D>(kt * 16 + c, ks * 4 + g)));
-          const v8 va =
-              as_vec8<T>(*(const u32x4 *)(cur + TILE + tile_off<D>(kt * 16 + c, ks * 4 + g)));
+          const v8 ka = as_vec8<T>(lds_read16(cur + koff[ks] + kt * 16 * D * 2));
+          const v8 va = as_vec8<T>(lds_read16(cur + TILE + koff[ks] + kt * 16 * D * 2));
           s[h][0] = mfma_16x16x32(ka, as_vec8<T>(qf[0][ks]), s[h][0]);
           s[h][1] = mfma_16x16x32(ka, as_vec8<T>(qf[1][ks]), s[h][1]);
           dp[h][0] = mfma_16x16x32(va, as_vec8<T>(df[0][ks]), dp[h][0]);
@@ -805,7 +816,7 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
       /* dQ^T += K^T dS^T over this half's 32 keys */
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) {
-        const v8 a = as_vec8<T>(read_kmajor_operand<D>(cur, 32 * kk, dt * 16, g, c));
+        const v8 a = as_vec8<T>(lds_read_kmajor(cur + kmoff[dt], 32 * kk * D * 2, (32 * kk + 16) * D * 2));
         acc[dt][0] = mfma_16x16x32(a, as_vec8<T>(dsf[0]), acc[dt][0]);
         acc[dt][1] = mfma_16x16x32(a, as_vec8<T>(dsf[1]), acc[dt][1]);
       }
@@ -821,13 +832,10 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
   const int n_interior = CAUSAL ? min(q0 / BN, n / BN) : n / BN;
   int j = 0;
   for (; j + 1 < n_interior; j += 2) {
-    step(Interior{}, lds_a, lds_b, j);
-    step(Interior{}, lds_b, lds_a, j + 1);
+    step(Interior{}, buf_a, buf_b, j);
+    step(Interior{}, buf_b, buf_a, j + 1);
   }
-  for (; j < nblocks; ++j) {
-    if ((j & 1) == 0) step(Edge{}, lds_a, lds_b, j);
-    else step(Edge{}, lds_b, lds_a, j);
-  }
+  for (; j < nblocks; ++j) step(Edge{}, (j & 1) ? buf_b : buf_a, (j & 1) ? buf_a : buf_b, j);
 
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
