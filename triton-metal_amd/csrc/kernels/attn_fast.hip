@@ -467,7 +467,9 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
     };
 
     /* operand o: (kk, dt) of the P V part for o < NA/QT, the row-sum ones
-     * first in each kk (no LDS wait behind them), then (kt, ks) of the S part */
+     * first in each kk (no LDS wait behind them), then (ks, kt) of the S part:
+     * k-step-major, so consecutive score MFMAs feed eight independent
+     * accumulators (kt-major gave two; 0.5-1% slower at configs 4 and 5) */
     u32x4 opnd[NM > 0 ? NM / QT : 1];
     auto read_op = [&](auto oo) {
       constexpr int o = decltype(oo)::value;
@@ -476,7 +478,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
         if constexpr (dt == DT) opnd[o] = ones;
         else opnd[o] = lds_read_kmajor(vrd + voff[dt], 32 * kk * D * 2, (32 * kk + 16) * D * 2);
       } else if constexpr (o < NM / QT) {
-        constexpr int b = o - NA / QT, kt = b / KS, ks = b % KS;
+        constexpr int b = o - NA / QT, kt = b % 4, ks = b / 4;
         opnd[o] = lds_read16(krd + koff[ks] + kt * 16 * D * 2);
       }
     };
@@ -531,7 +533,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
         constexpr int kk = o / (DT + 1), dt = (o % (DT + 1) + DT) % (DT + 1);
         acc[dt][qt] = mfma_16x16x32(as_vec8<T>(opnd[o]), as_vec8<T>(pf[qt][kk]), acc[dt][qt]);
       } else {
-        constexpr int b = o - NA / QT, kt = b / KS, ks = b % KS;
+        constexpr int b = o - NA / QT, kt = b % 4, ks = b / 4;
         sn[kt][qt] = mfma_16x16x32(as_vec8<T>(opnd[o]), as_vec8<T>(qf[qt][ks]), sn[kt][qt]);
       }
       if constexpr (SM)
