@@ -84,8 +84,8 @@ def profile_pass(core, ops):
     """One copy of COPY_BYTES (reads and writes that many bytes of HBM), then one
     dispatch each of attn_fwd, attn_bwd_preprocess, attn_bwd_dq, attn_bwd_dkdv at
     config 5, the bwd=atomic backward (attn_bwd_fused: accumulator clear, fused
-    kernel, dQ conversion) and the bwd=stash one (dK/dV with the dS stash, dQ
-    from it) at config 5, matmul_kernel at config 3 and sae_encode_kernel at 8192 x 2048 x 16384."""
+    kernel, dQ conversion), the bwd=stash one (dK/dV with the dS stash, dQ
+    from it) and the bwd=merged one (dK/dV and dQ in one grid) at config 5, matmul_kernel at config 3 and sae_encode_kernel at 8192 x 2048 x 16384."""
     from triton_metal.buffer import DeviceBuffer
     lib = core.compile_msl(COPY_SOURCE)
     kernel = core.load_kernel(lib, "tm_calibration_copy")
@@ -102,7 +102,7 @@ def profile_pass(core, ops):
     layer.run_forward()
     layer.run_backward()
     layer.free()
-    for mode in ("atomic", "stash"):
+    for mode in ("atomic", "stash", "merged"):
         fused = ops.AttentionLayer(B * H, S, D, "bf16", True, bwd=mode)
         for i, name in enumerate(("q", "k", "v", "do")):
             fused.buffers[name].write(normal_bf16((B * H, S, D), 100 + i))
@@ -517,6 +517,16 @@ def main():
             "frac_of_peak": round(f_bwd / (ms_s * 1e-3) / 1e12 / 2500, 4),
             "ms": round(ms_s, 4), "fused_ms": round(ks["attn_bwd_fused"]["ms"], 4),
             "vs_split": round(bwd_ms / ms_s, 3), "variant": ks["attn_bwd_fused"]["variant"]}
+        # the split's two kernels in one grid (bwd=merged: dQ workgroups fill the
+        # dK/dV tail; bit-identical to the split), beside the split as well
+        _, km = bench_attention(core, ops, B, H, S, D, True, 0, args.warmup, args.sample_ms,
+                                bwd="merged")
+        ms_m = km["attn_bwd_preprocess"]["ms"] + km["attn_bwd_fused"]["ms"]
+        components["fa2_bwd_merged"] = {
+            "tflops": round(f_bwd / (ms_m * 1e-3) / 1e12, 2),
+            "frac_of_peak": round(f_bwd / (ms_m * 1e-3) / 1e12 / 2500, 4),
+            "ms": round(ms_m, 4), "fused_ms": round(km["attn_bwd_fused"]["ms"], 4),
+            "vs_split": round(bwd_ms / ms_m, 3), "variant": km["attn_bwd_fused"]["variant"]}
         # fp16 variant of config 5 (the reference's own attention element type)
         _, k16 = bench_attention(core, ops, B, H, S, D, True, 0, args.warmup, args.sample_ms,
                                  element="f16")

@@ -18,15 +18,16 @@
  *       * a gfx950 code object image (tm_load_metallib),
  *       * HIP C++ source compiled at run time by hiprtc (tm_compile_msl), or
  *       * a built-in library spec "builtin [element=f32|f16|bf16]
- *         [head_dim=N] [causal=0|1] [bwd=split|atomic|stash]" (tm_compile_msl),
+ *         [head_dim=N] [causal=0|1] [bwd=split|atomic|stash|merged]" (tm_compile_msl),
  *         which names the library's hand-written gfx950 kernels for the dense
  *         hot path: matmul_kernel, attn_fwd, attn_bwd_preprocess, attn_bwd_dq,
  *         attn_bwd_dkdv, sae_encode_kernel (relu(x @ W + b),
  *         Sources/TritonMetalMLX/SAEEncoder.swift:29-40), tm_probe, and with
- *         bwd=atomic or bwd=stash attn_bwd_fused (the backward in one call
+ *         bwd=atomic, bwd=stash or bwd=merged attn_bwd_fused (the backward in one call
  *         that AttentionBackwardKernel.swift:27-41 names: Q, K, V, dO, dQ, dK,
  *         dV, L, Delta, sm_scale, stride_head, stride_seq, stride_lse, n_ctx;
- *         atomic sums dQ with fp32 atomics, stash keeps dS for a dQ pass).
+ *         atomic sums dQ with fp32 atomics, stash keeps dS for a dQ pass,
+ *         merged runs the split's dK/dV and dQ kernels in one grid).
  *   - a "buffer" is device memory in HBM (hipMalloc).  tm_buffer_contents
  *     gives it a host-addressable mirror (pinned host memory) that stands in
  *     for the reference's unified memory: while the mirror exists, host

@@ -133,7 +133,7 @@ def test_builtin_spec_round_trips_through_emit(core):
     ("builtin head_dim=0", "head_dim must be an integer in 1..128"),
     ("builtin head_dim=129", "head_dim must be an integer in 1..128"),
     ("builtin causal=2", "causal must be 0 or 1"),
-    ("builtin bwd=fast", "bwd must be split, atomic or stash"),
+    ("builtin bwd=fast", "bwd must be split, atomic, stash or merged"),
     ("builtin colour=red", "unknown key 'colour'"),
     ("builtin element", "expected key=value"),
 ])

@@ -2,7 +2,10 @@
   bwd=atomic  dK and dV from the same arithmetic as attn_bwd_dkdv, dQ
               accumulated across key blocks with fp32 atomics;
   bwd=stash   the dK/dV kernel also writes the rounded dS it computes, and a
-              dQ kernel reads it back (no recomputation, deterministic).
+              dQ kernel reads it back (no recomputation, deterministic);
+  bwd=merged  the split's dK/dV and dQ kernels in one grid (head_dim 128; at
+              64 the two kernels back to back): dQ, dK, dV bit-identical to
+              the split.
 
 The reference chose the split backward for determinism and named the atomic
 form as the unmeasured alternative (AttentionBackwardKernel.swift:27-41,
@@ -83,8 +86,10 @@ class _Run:
         _core.launch(kern, (1, self.heads, 1), 128, [B] * 9 + [F, I, I, I, I],
                      [self.h(x) for x in ("q", "k", "v", "do", "dq", "dk", "dv", "lse", "delta")] +
                      self.tail)
-        want = "tm_attn_fused_fast_" if self.bwd == "atomic" else "tm_attn_dkdv_stash_"
-        assert want in _core.kernel_variant(kern)
+        want = {"atomic": ("tm_attn_fused_fast_",), "stash": ("tm_attn_dkdv_stash_",),
+                # one merged grid at head_dim 128, the two split kernels at 64
+                "merged": ("tm_attn_bwd_merged_", "tm_attn_dkdv_fast_")}[self.bwd]
+        assert any(w in _core.kernel_variant(kern) for w in want)
         return self.grads()
 
     def free(self):
@@ -92,7 +97,7 @@ class _Run:
             b.free()
 
 
-BWD = ["atomic", "stash"]
+BWD = ["atomic", "stash", "merged"]
 
 
 @pytest.mark.parametrize("bwd", BWD)
@@ -115,6 +120,8 @@ def test_fused_backward_matches_oracle(bwd, element, dim, causal, seq, device):
     # per-block arithmetic and accumulation order are the same
     assert np.array_equal(fused["dk"], split["dk"])
     assert np.array_equal(fused["dv"], split["dv"])
+    if bwd == "merged":
+        assert np.array_equal(fused["dq"], split["dq"])
 
 
 @pytest.mark.parametrize("bwd", BWD)
@@ -136,7 +143,7 @@ def test_fused_backward_workspace_regrows_and_is_cleared(bwd, device):
         # the second launch sums the same partials in another order: one
         # rounding unit of the element type apart at most, not twice the value
         assert T.hybrid_error(again["dq"], fused["dq"]) <= 2 * T.U_BF16
-        if bwd == "stash":
+        if bwd in ("stash", "merged"):
             assert np.array_equal(again["dq"], fused["dq"])
         assert np.array_equal(again["dk"], fused["dk"])
 
@@ -159,6 +166,8 @@ def test_fused_backward_config5_full_size_against_split(bwd, device):
     assert np.array_equal(fused["dk"], split["dk"])
     assert np.array_equal(fused["dv"], split["dv"])
     assert np.all(np.isfinite(fused["dq"]))
+    if bwd == "merged":
+        assert np.array_equal(fused["dq"], split["dq"])
     # the two dQ come from differently ordered MFMA sums of dS (itself
     # recomputed in the other orientation, so a rounded dS may differ by one
     # unit): the same hybrid metric the oracle tests use, against the split

@@ -694,12 +694,12 @@ TM_PRE_FAST(f16_t, f16, 128)
  * offsets whose lane parts are computed once: with flat tile pointers (and a
  * branch between the two buffer phases in the masked loop) the kernel needed
  * 256 registers and spilled; so it needs 234 and runs 3% faster. */
+template <int D> struct DqLds { static constexpr int BYTES = 4 * 64 * D * 2; };
 template <typename T, int D, bool CAUSAL>
-TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
+TM_DEV void attn_dq_fast(const TmAttnDqArgs &p, char *lds, int wg, int nwg) {
   constexpr int BM = 128, BN = 64, QW = 32;
   constexpr int KS = D / 32;
   constexpr int TILE = BN * D * 2;
-  __shared__ __align__(1024) char lds[4 * TILE];
   const uint32_t buf_a = lds_addr(lds), buf_b = buf_a + 2 * TILE;
 
   typedef typename Vec8<T>::type v8;
@@ -708,7 +708,7 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p) {
   const int g = lane >> 4, c = lane & 15;
   const int n = p.n_ctx;
   const int nqb = (n + BM - 1) / BM;
-  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int logical = xcd_remap(wg, nwg);
   int bh, qb;
   if (CAUSAL) {
     causal_order(logical, nqb, p.heads, bh, qb);
@@ -1451,8 +1451,9 @@ TM_DEV void attn_dq_stash(const TmAttnFusedArgs &a) {
  * start from Delta, so they deliver Delta - dP, and the kernel carries
  * -dS = P (Delta - dP) with one multiply; the arithmetic is the same as that
  * kernel's (and its fused and stash forms'), so dK and dV are bit-identical. */
+struct Dkdv2wLds { static constexpr int BYTES = 128 * 128 * 2 + 2 * (2 * 32 * 128 * 2 + 32 * 8); };
 template <typename T, int D, bool CAUSAL>
-TM_DEV void attn_dkdv_2w(const TmAttnDkdvArgs &p) {
+TM_DEV void attn_dkdv_2w(const TmAttnDkdvArgs &p, char *lds, int wg, int nwg) {
   static_assert(D == 128, "two-wave dK/dV is built for head_dim 128");
   constexpr int BN = 128, KW = 32, BM = 32;
   constexpr int KS = D / 32, DT = D / 16;
@@ -1460,7 +1461,7 @@ TM_DEV void attn_dkdv_2w(const TmAttnDkdvArgs &p) {
   constexpr int VT = BN * D * 2;
   constexpr int STATS = 2 * TILE;
   constexpr int BUF = 2 * TILE + BM * 8;
-  __shared__ __align__(1024) char lds[VT + 2 * BUF];
+  static_assert(VT + 2 * BUF <= Dkdv2wLds::BYTES, "LDS");
   const uint32_t vbase = lds_addr(lds), buf0 = vbase + VT, buf1 = buf0 + BUF;
 
   typedef typename Vec8<T>::type v8;
@@ -1469,7 +1470,7 @@ TM_DEV void attn_dkdv_2w(const TmAttnDkdvArgs &p) {
   const int g = lane >> 4, c = lane & 15;
   const int n = p.n_ctx;
   const int nkb = (n + BN - 1) / BN;
-  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int logical = xcd_remap(wg, nwg);
   int bh, kb;
   if (CAUSAL) {
     causal_order(logical, nkb, p.heads, bh, kb);
@@ -1654,7 +1655,8 @@ TM_DEV void attn_dkdv_2w(const TmAttnDkdvArgs &p) {
 #define TM_BWD_FAST(T, TN, D, CAUSAL, CN)                                                     \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void  \
   tm_attn_dq_fast_##TN##_d##D##CN(TmAttnDqArgs p) {                                           \
-    attn_dq_fast<T, D, CAUSAL>(p);                                                            \
+    __shared__ __align__(1024) char lds[DqLds<D>::BYTES];                                     \
+    attn_dq_fast<T, D, CAUSAL>(p, lds, blockIdx.x, gridDim.x);                                \
   }                                                                                           \
   TM_DKDV_FAST_##D(T, TN, CAUSAL, CN)
 /* head_dim 128: the two-waves-per-SIMD kernel (0.99-1.03 ms at B4 H32 S4096
@@ -1664,7 +1666,41 @@ TM_DEV void attn_dkdv_2w(const TmAttnDkdvArgs &p) {
 #define TM_DKDV_FAST_128(T, TN, CAUSAL, CN)                                                   \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void  \
   tm_attn_dkdv_fast_##TN##_d128##CN(TmAttnDkdvArgs p) {                                       \
-    attn_dkdv_2w<T, 128, CAUSAL>(p);                                                          \
+    __shared__ __align__(1024) char lds[Dkdv2wLds::BYTES];                                    \
+    attn_dkdv_2w<T, 128, CAUSAL>(p, lds, blockIdx.x, gridDim.x);                              \
+  }                                                                                           \
+  /* bwd=merged: one grid, the dK/dV workgroups first (the heavier ones), then    \
+   * the dQ workgroups, each running the split kernels' code over one LDS array  \
+   * (the larger of the two), so dQ work fills the dK/dV tail and the results    \
+   * are bit-identical to the split's.  The dQ part's xcd_remap assumes the     \
+   * dK/dV part's workgroup count is a multiple of 8 (otherwise only the L2     \
+   * locality of its mapping changes). */                                        \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void  \
+  tm_attn_bwd_merged_##TN##_d128##CN(TmAttnFusedArgs a) {                                     \
+    constexpr int BYTES =                                                                     \
+        Dkdv2wLds::BYTES > DqLds<128>::BYTES ? Dkdv2wLds::BYTES : DqLds<128>::BYTES;          \
+    __shared__ __align__(1024) char lds[BYTES];                                               \
+    const int nkv = (int)gridDim.x / 2;                                                       \
+    if ((int)blockIdx.x < nkv) {                                                              \
+      attn_dkdv_2w<T, 128, CAUSAL>(a.kv, lds, blockIdx.x, nkv);                               \
+    } else {                                                                                  \
+      TmAttnDqArgs q{};                                                                       \
+      q.q = a.kv.q;                                                                           \
+      q.k = a.kv.k;                                                                           \
+      q.v = a.kv.v;                                                                           \
+      q.dout = a.kv.dout;                                                                     \
+      q.dq = a.dq;                                                                            \
+      q.lse = a.kv.lse;                                                                       \
+      q.delta = a.kv.delta;                                                                   \
+      q.sm_scale = a.kv.sm_scale;                                                             \
+      q.stride_head = a.kv.stride_head;                                                       \
+      q.stride_seq = a.kv.stride_seq;                                                         \
+      q.stride_lse = a.kv.stride_lse;                                                         \
+      q.n_ctx = a.kv.n_ctx;                                                                   \
+      q.head_dim = a.kv.head_dim;                                                             \
+      q.heads = a.kv.heads;                                                                   \
+      attn_dq_fast<T, 128, CAUSAL>(q, lds, blockIdx.x - nkv, (int)gridDim.x - nkv);           \
+    }                                                                                         \
   }
 #define TM_DKDV_FAST_64(T, TN, CAUSAL, CN)                                                    \
   extern "C" __global__ __launch_bounds__(256) void tm_attn_dkdv_fast_##TN##_d64##CN(         \

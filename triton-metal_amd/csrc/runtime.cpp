@@ -223,14 +223,19 @@ struct BuiltinSpec {
    * floating-point atomics (not deterministic); stash: the dK/dV kernel
    * writes the rounded dS it computes, and a dQ kernel reads it back instead
    * of recomputing S and dP (deterministic; heads * n_ctx^2 * 2 bytes of
-   * workspace).  The reference's split (attn_bwd_dq + attn_bwd_dkdv) stays
-   * available in every library. */
-  enum class Bwd { Split, Atomic, Stash } bwd = Bwd::Split;
+   * workspace); merged: the split's dK/dV and dQ kernels in one grid (dQ
+   * workgroups fill the dK/dV tail; deterministic, bit-identical to the
+   * split, no workspace).  The reference's split (attn_bwd_dq +
+   * attn_bwd_dkdv) stays available in every library. */
+  enum class Bwd { Split, Atomic, Stash, Merged } bwd = Bwd::Split;
 
   std::string text() const {
     return format("builtin element=%s head_dim=%d causal=%d%s", element_name(element), head_dim,
                   causal ? 1 : 0,
-                  bwd == Bwd::Atomic ? " bwd=atomic" : bwd == Bwd::Stash ? " bwd=stash" : "");
+                  bwd == Bwd::Atomic   ? " bwd=atomic"
+                  : bwd == Bwd::Stash  ? " bwd=stash"
+                  : bwd == Bwd::Merged ? " bwd=merged"
+                                       : "");
   }
 };
 
@@ -383,7 +388,8 @@ BuiltinSpec parse_spec(const char *text) {
       if (value == "split") spec.bwd = BuiltinSpec::Bwd::Split;
       else if (value == "atomic") spec.bwd = BuiltinSpec::Bwd::Atomic;
       else if (value == "stash") spec.bwd = BuiltinSpec::Bwd::Stash;
-      else throw TmError("built-in library spec: bwd must be split, atomic or stash, got '" + value +
+      else if (value == "merged") spec.bwd = BuiltinSpec::Bwd::Merged;
+      else throw TmError("built-in library spec: bwd must be split, atomic, stash or merged, got '" + value +
                          "'");
     } else {
       throw TmError("built-in library spec: unknown key '" + key + "'");
@@ -857,6 +863,57 @@ void plan_stash_backward(Plan &plan, const BuiltinSpec &spec, const TmAttnDkdvAr
   plan.sequence = {kv_pass, dq_pass};
 }
 
+/* attn_bwd_fused under bwd=merged: at head_dim 128 one dispatch of
+ * tm_attn_bwd_merged_* over the dK/dV grid followed by the dQ grid (both
+ * cdiv(n_ctx, 128) * heads workgroups of 256 threads); at head_dim 64, whose
+ * dK/dV kernel runs one wave per SIMD and dQ three, the two split kernels back
+ * to back.  Either way dQ, dK and dV are the split's, bit for bit. */
+void plan_merged_backward(Plan &plan, const BuiltinSpec &spec, const TmAttnDkdvArgs &kv, void *dq) {
+  const char *el = element_name(spec.element);
+  const char *cn = spec.causal ? "_causal" : "";
+  const unsigned wgs = (unsigned)(cdiv(kv.n_ctx, 128) * kv.heads);
+  TmAttnDqArgs q{};
+  q.q = kv.q;
+  q.k = kv.k;
+  q.v = kv.v;
+  q.dout = kv.dout;
+  q.dq = dq;
+  q.lse = kv.lse;
+  q.delta = kv.delta;
+  q.sm_scale = kv.sm_scale;
+  q.stride_head = kv.stride_head;
+  q.stride_seq = kv.stride_seq;
+  q.stride_lse = kv.stride_lse;
+  q.n_ctx = kv.n_ctx;
+  q.head_dim = kv.head_dim;
+  q.heads = kv.heads;
+  if (spec.head_dim == 128) {
+    TmAttnFusedArgs f{};
+    f.kv = kv;
+    f.dq = dq;
+    plan.variant = format("tm_attn_bwd_merged_%s_d128%s", el, cn);
+    plan.grid[0] = 2 * wgs;
+    plan.block = 256;
+    set_kernarg(plan, f);
+    plan.function = builtin_function(plan.variant);
+    return;
+  }
+  Plan kv_pass, dq_pass;
+  kv_pass.variant = format("tm_attn_dkdv_fast_%s_d%d%s", el, spec.head_dim, cn);
+  kv_pass.grid[0] = wgs;
+  kv_pass.block = 256;
+  set_kernarg(kv_pass, kv);
+  dq_pass.variant = format("tm_attn_dq_fast_%s_d%d%s", el, spec.head_dim, cn);
+  dq_pass.grid[0] = wgs;
+  dq_pass.block = 256;
+  set_kernarg(dq_pass, q);
+  for (Plan *part : {&kv_pass, &dq_pass}) part->function = builtin_function(part->variant);
+  plan.variant = kv_pass.variant;
+  plan.function = kv_pass.function;
+  plan.block = kv_pass.block;
+  plan.sequence = {kv_pass, dq_pass};
+}
+
 /* Ranges to split a generic attention kernel's walk into when its grid of
  * `wgs` 64-row workgroups cannot fill the chip twice: enough to (at most 16,
  * each at least two 32-row blocks of the `n_ctx` walked); 1 for no split. */
@@ -1226,6 +1283,10 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
       kv.sm_scale = sm_scale;
       kv.head_dim = spec.head_dim;
       kv.heads = (int32_t)heads;
+      if (spec.bwd == BuiltinSpec::Bwd::Merged) {
+        plan_merged_backward(plan, spec, kv, args[4].buffer->ptr);
+        return plan;
+      }
       const bool stash = spec.bwd == BuiltinSpec::Bwd::Stash;
       /* atomic: the fp32 dQ accumulator; stash: dS^T per head as [query
        * blocks of 32, rounded up to whole 256-query blocks][keys rounded up
@@ -1724,7 +1785,8 @@ int64_t tm_load_kernel(int64_t library, const char *name) {
     if (info->id == Builtin::AttnFused && lib->spec.bwd == BuiltinSpec::Bwd::Split)
       throw TmError("kernel 'attn_bwd_fused' is offered only by built-in libraries whose spec "
                     "has bwd=atomic (dQ summed with floating-point atomics, not deterministic) "
-                    "or bwd=stash (dS kept in a workspace for the dQ pass)");
+                    "or bwd=stash (dS kept in a workspace for the dQ pass) or bwd=merged (the "
+                    "split's dK/dV and dQ kernels in one grid)");
     k->builtin = info->id;
     /* load the kernel images now, so that launches (tm_launch_noalloc among
      * them) load no code; a failure here resurfaces at the first launch */

@@ -104,12 +104,13 @@ struct TmAttnDkdvArgs {
   int32_t splits;
 };
 
-/* attn_bwd_fused (built-in libraries with bwd=atomic or bwd=stash; no
+/* attn_bwd_fused (built-in libraries with bwd=atomic, bwd=stash or bwd=merged; no
  * reference kernel — the single-pass variant the reference names at
  * AttentionBackwardKernel.swift:27-41 and docs/COMPARISON.md:151-154): the
  * dK/dV kernel's arguments plus, for bwd=atomic, dQ's fp32 accumulator
  * ([heads][n_ctx][head_dim] dense, zeroed before the launch), or, for
- * bwd=stash, dQ and the dS^T stash the dK/dV pass writes for the dQ pass. */
+ * bwd=stash, dQ and the dS^T stash the dK/dV pass writes for the dQ pass, or,
+ * for bwd=merged, dQ. */
 struct TmAttnFusedArgs {
   TmAttnDkdvArgs kv;
   float *dq_acc;   /* bwd=atomic */
