@@ -1622,7 +1622,10 @@ TM_DEV void attn_dkdv_2w(const TmAttnDkdvArgs &p, char *lds, int wg, int nwg) {
   auto step = [&](auto edge_tag, int i) {
     const uint32_t cur = (i & 1) ? buf1 : buf0, nxt = (i & 1) ? buf0 : buf1;
     if (i + 1 < nblocks) stage(nxt, i + 1);
-    block(edge_tag, cur, i);
+    /* causal: a block whose every query precedes the wave's first key adds
+     * exact zeros; the wave skips its arithmetic (not its copies and barrier),
+     * which changes no bit of dK or dV (0.5-1% faster at config 5) */
+    if (!CAUSAL || q_start + (i + 1) * BM > kw0) block(edge_tag, cur, i);
     wait_vmem();
     __syncthreads();
   };
