@@ -380,7 +380,7 @@ def _head_backward64(q, k, v, d_out, scale):
 def test_config5_causal_forward_backward_full_size(device, element):
     """B4 H32 S4096 D128 causal in bf16 (the benchmark's element type) and f16
     (the reference's own attention element type), N(0,1), scale 1/sqrt(128): O,
-    LSE, dQ, dK, dV.  Three heads against fp64 (2e-2 absolute on O and LSE, 2e-2 hybrid on
+    LSE, dQ, dK, dV.  Every head against fp64 (2e-2 absolute on O and LSE, 2e-2 hybrid on
     the gradients); every head through size-independent identities of causal
     attention: O[0] = V[0], dQ[0] = 0, sum_j dK_j = 0, sum_j dV_j = sum_i dO_i."""
     bh, seq, dim = 128, 4096, 128
@@ -395,14 +395,16 @@ def test_config5_causal_forward_backward_full_size(device, element):
         r.free()
     print("config5 variants:", variants)
     scale = 1 / math.sqrt(dim)
-    for h in (0, 63, 127):
+    worst = {"dq": 0.0, "dk": 0.0, "dv": 0.0}
+    for h in range(bh):
         o64, l64, dq64, dk64, dv64 = _head_backward64(q[h], k[h], v[h], d_out[h], scale)
         assert T.max_abs_error(o[h], o64) <= 2e-2
         assert T.max_abs_error(lse[h] * LN2, l64) <= 2e-2
         for name, got, want in (("dq", dq[h], dq64), ("dk", dk[h], dk64), ("dv", dv[h], dv64)):
             err = T.hybrid_error(got, want)
-            print(f"head {h} {name} hybrid {err:.3e}")
+            worst[name] = max(worst[name], err)
             assert err <= 2e-2, (h, name)
+    print("config5 worst hybrid error over all heads:", {n: f"{e:.3e}" for n, e in worst.items()})
     assert np.all(np.isfinite(o)) and np.all(np.isfinite(dq))
     assert np.all(np.isfinite(dk)) and np.all(np.isfinite(dv))
     assert T.max_abs_error(o[:, 0], v[:, 0]) <= 1e-2
