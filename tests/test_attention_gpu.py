@@ -334,7 +334,7 @@ def test_config2_training_steps_match_numpy_autograd(device):
 def test_config4_bf16_forward_full_size(device):
     """B8 H16 S1024 D64 bf16, non-causal, N(0,1), scale 1/8: O and the natural-log
     logsumexp (L*ln2) of every head within 2e-2 absolute of an fp32 BLAS
-    reference from the same bf16 inputs; 4 heads also against fp64."""
+    reference from the same bf16 inputs, and every head also against fp64."""
     bh, seq, dim = 128, 1024, 64
     q, k, v = normal_inputs(bh, seq, dim, "bf16", seed=4, count=3)
     r = Runner(bh, seq, dim, "bf16")
@@ -351,7 +351,7 @@ def test_config4_bf16_forward_full_size(device):
     lse_nat = (peak[..., 0] + np.log(tot[..., 0]))
     assert T.max_abs_error(o, o32) <= 2e-2
     assert T.max_abs_error(lse * LN2, lse_nat) <= 2e-2
-    for h in (0, 37, 90, 127):
+    for h in range(bh):
         o64, _, l64 = R.attention_forward(q[h:h + 1], k[h:h + 1], v[h:h + 1], scale)
         assert T.max_abs_error(o[h:h + 1], o64) <= 2e-2
         assert T.max_abs_error(lse[h:h + 1] * LN2, l64 * LN2) <= 2e-2
