@@ -486,7 +486,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
      * as fma, exp, pack and OR on four consecutive slots */
     uint32_t big = 0;       /* OR of the packed P words */
     float px[2], pe[2];
-    uint32_t wd = 0;
+    uint32_t wd = 0, wprev = 0;
     auto vslot = [&](auto vv) {
       constexpr int v = decltype(vv)::value;
       constexpr int u = v / 4, beat = v % 4, qt = u / 8, kk = (u / 4) % 2, w = u % 4;
@@ -505,8 +505,10 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
         wd = pack2<T>(pe[0], pe[1]);
         pin(wd);
         pn[qt][kk][w] = wd;
+      } else if constexpr (u % 2 == 0) {
+        wprev = wd; /* ORed with the next pair's word: one v_or3 per two words */
       } else {
-        big |= wd;
+        big = big | wprev | wd;
         pin(big);
       }
     };
