@@ -17,9 +17,15 @@ Per-kernel durations come from HIP events recorded on the library's stream
 around back-to-back dispatches (tm_launch_timed).
 
 The CPU baseline times the oracle's float32 BLAS restatement of the reference's
-attention forward and backward (oracle/reference.py attention_head_f32, after
-attention_training.py:170-187, causal) on a bounded sample of the workload on
-the host cores.
+attention forward and backward (oracle/reference.py
+attention_head_causal_blocked_f32, after attention_training.py:170-187, causal)
+on a bounded sample of the workload on the host cores: one warm-up, median of 3.
+
+After its timings every measured configuration is checked: sampled heads of O,
+L, Delta, dQ, dK, dV and sampled rows of every GEMM and SAE output against fp64
+from the same rounded inputs (the reference's verify-before-timing rule,
+GEMMBenchmark.swift:320-375).  A miss prints the errors and exits 1 with no
+JSON line; the line carries the errors under "verified".
 Prints ONE JSON line.
 """
 
@@ -84,8 +90,8 @@ def profile_pass(core, ops):
     """One copy of COPY_BYTES (reads and writes that many bytes of HBM), then one
     dispatch each of attn_fwd, attn_bwd_preprocess, attn_bwd_dq, attn_bwd_dkdv at
     config 5, the bwd=atomic backward (attn_bwd_fused: accumulator clear, fused
-    kernel, dQ conversion), the bwd=stash one (dK/dV with the dS stash, dQ
-    from it) and the bwd=merged one (dK/dV and dQ in one grid) at config 5, matmul_kernel at config 3 and sae_encode_kernel at 8192 x 2048 x 16384."""
+    kernel, dQ conversion) at config 5, matmul_kernel at config 3 and
+    sae_encode_kernel at 8192 x 2048 x 16384."""
     from triton_metal.buffer import DeviceBuffer
     lib = core.compile_msl(COPY_SOURCE)
     kernel = core.load_kernel(lib, "tm_calibration_copy")
@@ -102,7 +108,7 @@ def profile_pass(core, ops):
     layer.run_forward()
     layer.run_backward()
     layer.free()
-    for mode in ("atomic", "stash", "merged"):
+    for mode in ("atomic",):
         fused = ops.AttentionLayer(B * H, S, D, "bf16", True, bwd=mode)
         for i, name in enumerate(("q", "k", "v", "do")):
             fused.buffers[name].write(normal_bf16((B * H, S, D), 100 + i))
@@ -200,13 +206,136 @@ def kernel_ms(core, kernel, grid, kinds, values, sample_ms):
     return samples[1]
 
 
+# --------------------------------------------------------------------------- #
+# Verification of what was timed (the reference checks every benchmarked
+# configuration against a CPU reference before believing its timings:
+# GEMMBenchmark.swift:320-375, AttentionBackwardBenchmark.swift:263-414).
+# fp64 numpy, outside every timed region; a miss ends the run without a line.
+# --------------------------------------------------------------------------- #
+
+#: bounds: O and the natural-log logsumexp within 2e-2 absolute, Delta, dQ,
+#: dK, dV and GEMM rows within 2e-2 hybrid (|a - b| / max(1, |b|)) of fp64
+#: computed from the same rounded inputs: north_star's 16-bit bar.  fp32
+#: GEMMs: 1e-5 relative, max|a - b| / max|b| (its fp32 bar).
+TOL_16 = 2e-2
+TOL_F32 = 1e-5
+#: fp32 attention: the reference's 2e-5 forward bound (AttentionTests.swift) with
+#: room for the backward's longer sums
+TOL_F32_ATTN = 1e-4
+
+
+def _hybrid(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    if not np.all(np.isfinite(a)):
+        return float("inf")
+    return float(np.max(np.abs(a - b) / np.maximum(1.0, np.abs(b))))
+
+
+def _relative(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    if not np.all(np.isfinite(a)):
+        return float("inf")
+    return float(np.max(np.abs(a - b)) / max(float(np.max(np.abs(b))), 1e-30))
+
+
+def _abs(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    if not np.all(np.isfinite(a)):
+        return float("inf")
+    return float(np.max(np.abs(a - b)))
+
+
+def _attention_head64(q, k, v, d_out, scale, causal):
+    """One head in fp64: O, natural-log LSE, Delta, dQ, dK, dV (the
+    definitions: softmax(Q K^T * scale) V and its gradients for upstream dO)."""
+    q, k, v = (np.asarray(x, np.float64) for x in (q, k, v))
+    s = (q @ k.T) * scale
+    if causal:
+        s[np.triu_indices(s.shape[0], 1)] = -np.inf
+    peak = s.max(-1, keepdims=True)
+    e = np.exp(s - peak)
+    total = e.sum(-1, keepdims=True)
+    p = e / total
+    o = p @ v
+    out = {"o": o, "lse": peak[:, 0] + np.log(total[:, 0])}
+    if d_out is not None:
+        d_out = np.asarray(d_out, np.float64)
+        delta = np.sum(d_out * o, -1)
+        ds = p * (d_out @ v.T - delta[:, None])
+        out.update(delta=delta, dq=ds @ k * scale, dk=ds.T @ q * scale, dv=p.T @ d_out)
+    return out
+
+
+class Verifier:
+    """Collects the worst error of every checked output; `failures` lists the
+    outputs over their bound."""
+
+    def __init__(self):
+        self.record = {}
+        self.failures = []
+
+    def add(self, case, name, err, bound):
+        rec = self.record.setdefault(case, {})
+        rec[name] = max(rec.get(name, 0.0), round(err, 6))
+        rec.setdefault("bound", {})[name] = bound
+        if not err <= bound:
+            self.failures.append(f"{case}.{name}: error {err:.3e} > {bound:g}")
+
+
+def _read_rows(buf, first, count, row_elems):
+    """Rows [first, first + count) of a buffer as float32 (bf16 decoded)."""
+    from triton_metal import _core
+    from triton_metal.buffer import _NUMPY, bf16_values
+    out = np.empty(count * row_elems, dtype=_NUMPY[buf.dtype])
+    _core.buffer_read(buf.tm_handle, first * row_elems * buf.itemsize, out.ctypes.data, out.nbytes)
+    if buf.dtype == "bfloat16":
+        return bf16_values(out).reshape(count, row_elems)
+    return out.astype(np.float32).reshape(count, row_elems)
+
+
+def _input_values(bits, element):
+    """What a buffer of `element` holds after write() of bf16 words' values."""
+    from triton_metal.buffer import bf16_values
+    x = bf16_values(bits)
+    return x.astype(np.float16).astype(np.float32) if element == "f16" else x
+
+
+def verify_attention(layer, host, heads_to_check, verifier, case, backward):
+    """The checked heads' outputs, read back after the timed runs, against fp64
+    from the same rounded inputs."""
+    seq, dim, el = layer.seq, layer.dim, layer.element
+    tol = TOL_F32_ATTN if el == "f32" else TOL_16
+    for h in heads_to_check:
+        x = {n: _input_values(host[n][h], el) for n in host}
+        want = _attention_head64(x["q"], x["k"], x["v"], x["do"] if backward else None,
+                                 layer.scale, layer.causal)
+        o = _read_rows(layer.buffers["o"], h * seq, seq, dim)
+        lse = _read_rows(layer.buffers["lse"], h, 1, seq)[0]
+        verifier.add(case, "o", _abs(o, want["o"]), tol)
+        verifier.add(case, "lse", _abs(lse * math.log(2.0), want["lse"]), tol)
+        if backward:
+            # Delta is defined on the O the forward stored (element type), the
+            # O attn_bwd_preprocess reads
+            delta = _read_rows(layer.buffers["delta"], h, 1, seq)[0]
+            want_delta = np.sum(o.astype(np.float64) * x["do"].astype(np.float64), -1)
+            verifier.add(case, "delta", _hybrid(delta, want_delta), tol)
+            for name in ("dq", "dk", "dv"):
+                got = _read_rows(layer.buffers[name], h * seq, seq, dim)
+                verifier.add(case, name, _hybrid(got, want[name]), tol)
+    verifier.record[case]["heads"] = list(heads_to_check)
+
+
 def bench_attention(core, ops, batch, heads, seq, dim, causal, steps, warmup, sample_ms,
-                    backward=True, element="bf16", bwd="split"):
+                    backward=True, element="bf16", bwd="split", verifier=None, case=None,
+                    check_heads=()):
     bh = batch * heads
     layer = ops.AttentionLayer(bh, seq, dim, element, causal, bwd=bwd)
+    host = {}
     try:
         for i, name in enumerate(("q", "k", "v", "do")):
             x = normal_bf16((bh, seq, dim), 100 + i)
+            if check_heads:
+                host[name] = {h: x[h].copy() for h in check_heads}
             if element != "bf16":
                 from triton_metal.buffer import bf16_values
                 x = bf16_values(x)  # the same N(0,1) values, converted by write()
@@ -240,20 +369,28 @@ def bench_attention(core, ops, batch, heads, seq, dim, causal, steps, warmup, sa
                 "ms": kernel_ms(core, kern[name], grid, kinds, values, sample_ms),
                 "variant": core.kernel_variant(kern[name]),
             }
+        core.synchronize()
+        if verifier is not None and check_heads:
+            verify_attention(layer, host, check_heads, verifier, case, backward)
     finally:
         layer.free()
     return wall_ms, per_kernel
 
 
-def bench_gemm(core, ops, n, warmup, sample_ms, element="bf16", layout="nn"):
+def bench_gemm(core, ops, n, warmup, sample_ms, element="bf16", layout="nn", verifier=None,
+               case=None, check_rows=64):
     """n^3 GEMM on N(0,1) operands.  layout "nt": B is passed transposed
-    (stride_bk = 1, the x @ W^T layout); "tn": A transposed (stride_am = 1)."""
+    (stride_bk = 1, the x @ W^T layout); "tn": A transposed (stride_am = 1).
+    After the timing, `check_rows` sampled rows of C against fp64."""
     from triton_metal.buffer import DeviceBuffer, bf16_values
     dtype = {"bf16": "bfloat16", "f16": "float16", "f32": "float32"}[element]
     strides = {"nn": (n, 1, n, 1, n, 1), "nt": (n, 1, 1, n, n, 1), "tn": (1, n, n, 1, n, 1)}[layout]
+    host = {}
 
     def operand(seed):
         x = normal_bf16((n, n), seed)
+        host[seed] = bf16_values(x) if element == "bf16" else bf16_values(x).astype(
+            np.float16 if element == "f16" else np.float32).astype(np.float32)
         return DeviceBuffer((n, n), dtype).write(x if element == "bf16" else bf16_values(x))
 
     a, b = operand(1), operand(2)
@@ -266,6 +403,20 @@ def bench_gemm(core, ops, n, warmup, sample_ms, element="bf16", layout="nn"):
         core.synchronize()
         ms = kernel_ms(core, kernel, grid, kinds, values, sample_ms)
         variant = core.kernel_variant(kernel)
+        core.synchronize()
+        if verifier is not None:
+            rows = np.sort(np.random.default_rng(n).choice(n, min(check_rows, n), replace=False))
+            a_rows = host[1][:, rows].T if layout == "tn" else host[1][rows]
+            b_full = host[2].T if layout == "nt" else host[2]
+            want = a_rows.astype(np.float64) @ b_full.astype(np.float64)
+            got = np.stack([_read_rows(c, int(r), 1, n)[0] for r in rows])
+            if element == "f32":
+                # north_star's fp32 bar: 1e-5 relative, max|a - b| / max|b| (the
+                # reference's relative_error, attention_training.py:250-252)
+                verifier.add(case, "c_rows_rel", _relative(got, want), TOL_F32)
+            else:
+                verifier.add(case, "c_rows", _hybrid(got, want), TOL_16)
+            verifier.record[case]["rows"] = len(rows)
     finally:
         for x in (a, b, c):
             x.free()
@@ -285,12 +436,15 @@ def gemm_flops(m, n, k) -> float:
     return 2.0 * m * n * k
 
 
-def bench_sae(core, ops, rows, model, features, warmup, sample_ms):
-    """The fused encoder relu(x @ W_enc + b_enc) in bf16 (sae_encode_kernel)."""
-    from triton_metal.buffer import DeviceBuffer
-    x = DeviceBuffer((rows, model), "bfloat16").write(normal_bf16((rows, model), 3))
-    w = DeviceBuffer((model, features), "bfloat16").write(normal_bf16((model, features), 4))
-    b = DeviceBuffer((features,), "bfloat16").write(normal_bf16((features,), 5))
+def bench_sae(core, ops, rows, model, features, warmup, sample_ms, verifier=None, case=None):
+    """The fused encoder relu(x @ W_enc + b_enc) in bf16 (sae_encode_kernel);
+    afterwards 64 sampled rows against fp64."""
+    from triton_metal.buffer import DeviceBuffer, bf16_values
+    hx, hw, hb = (normal_bf16((rows, model), 3), normal_bf16((model, features), 4),
+                  normal_bf16((features,), 5))
+    x = DeviceBuffer((rows, model), "bfloat16").write(hx)
+    w = DeviceBuffer((model, features), "bfloat16").write(hw)
+    b = DeviceBuffer((features,), "bfloat16").write(hb)
     out = DeviceBuffer((rows, features), "bfloat16")
     try:
         enc = ops.SAEEncoder("bf16")
@@ -300,6 +454,15 @@ def bench_sae(core, ops, rows, model, features, warmup, sample_ms):
         core.synchronize()
         ms = kernel_ms(core, enc.kernel, grid, kinds, values, sample_ms)
         variant = core.kernel_variant(enc.kernel)
+        core.synchronize()
+        if verifier is not None:
+            sel = np.sort(np.random.default_rng(rows).choice(rows, 64, replace=False))
+            want = np.maximum(bf16_values(hx[sel]).astype(np.float64)
+                              @ bf16_values(hw).astype(np.float64)
+                              + bf16_values(hb).astype(np.float64)[None, :], 0.0)
+            got = np.stack([_read_rows(out, int(r), 1, features)[0] for r in sel])
+            verifier.add(case, "out_rows", _hybrid(got, want), TOL_16)
+            verifier.record[case]["rows"] = len(sel)
     finally:
         for a in (x, w, b, out):
             a.free()
@@ -363,30 +526,40 @@ def bench_latency_configs(core, ops, sample_ms):
 
 def cpu_baseline(target_seconds):
     """The oracle's float32 BLAS restatement of the reference's attention forward
-    and backward (oracle.reference.attention_head_f32; attention_training.py:
-    170-187 with the causal mask), one (batch, head) of config 5 at a time
-    (S=4096, D=128), repeated until about `target_seconds` of CPU work; TFLOP/s
-    under the same FLOP convention."""
+    and backward (oracle.reference.attention_head_causal_blocked_f32;
+    attention_training.py:170-187 with the causal mask, by blocks of 512 query
+    rows over the keys they can see), one (batch, head) of config 5 at a time
+    (S=4096, D=128).  The reference's timing method (GEMMBenchmark.swift:
+    250-277): one warm-up head, then 3 samples of about target_seconds / 3 each,
+    the median sample's rate reported.  TFLOP/s credited with the causal half
+    of the reference's FLOPs, as the GPU figure is; the blocked form executes
+    36/64 of the full square, stated in `sample`."""
     from oracle import reference as R  # the CPU baseline is the oracle, timed
 
-    seq, dim = 4096, 128
+    seq, dim, block = 4096, 128, 512
     scale = np.float32(1 / math.sqrt(dim))
     rng = np.random.default_rng(0)
-
-    def one_head(q, k, v, d_out):
-        return R.attention_head_f32(q, k, v, d_out, scale, causal=True)
-
     q, k, v, d_out = (rng.standard_normal((seq, dim), dtype=np.float32) for _ in range(4))
-    heads = 0
-    t0 = time.perf_counter()
-    while True:
-        one_head(q, k, v, d_out)
-        heads += 1
-        elapsed = time.perf_counter() - t0
-        if elapsed >= target_seconds or heads >= 2048:
-            break
-    flops = attention_flops(heads, seq, dim, True) + attention_flops(heads, seq, dim, True,
-                                                                     backward=True)
+
+    def one_head():
+        return R.attention_head_causal_blocked_f32(q, k, v, d_out, scale, block=block)
+
+    one_head()  # warm-up: BLAS thread pool, page faults of the work arrays
+    samples = []
+    for _ in range(3):
+        heads = 0
+        t0 = time.perf_counter()
+        while True:
+            one_head()
+            heads += 1
+            elapsed = time.perf_counter() - t0
+            if elapsed >= target_seconds / 3 or heads >= 512:
+                break
+        flops = attention_flops(heads, seq, dim, True) + attention_flops(heads, seq, dim, True,
+                                                                         backward=True)
+        samples.append((flops / elapsed / 1e12, heads, elapsed))
+    samples.sort()
+    rate, heads, elapsed = samples[1]
     host_cpus = os.cpu_count()
     blas_threads, blas_library = None, None
     try:
@@ -397,8 +570,10 @@ def cpu_baseline(target_seconds):
             blas_library = info[0].get("internal_api")
     except Exception:
         pass
+    nb = seq // block
+    executed = nb * (nb + 1) // 2 / (nb * nb)
     return {
-        "value": round(flops / elapsed / 1e12, 6),
+        "value": round(rate, 6),
         "unit": "TFLOP/s",
         # the threads the BLAS calls ran on (the whole of the work); the host's
         # logical CPUs beside it
@@ -407,8 +582,12 @@ def cpu_baseline(target_seconds):
         "blas_threads": blas_threads,
         "blas_library": blas_library,
         "kind": "port",
-        "sample": (f"{heads} (batch,head) slices of config 5 (S4096 D128 causal) forward+backward "
-                   f"in numpy fp32 BLAS, {elapsed:.1f} s"),
+        "samples_tflops": [round(x[0], 6) for x in sorted(samples, key=lambda x: x[0])],
+        "sample": (f"(batch,head) slices of config 5 (S4096 D128 causal) forward+backward in numpy "
+                   f"fp32 BLAS by {block}-row query blocks over visible keys only ({executed:.4f} "
+                   f"of the full S^2 products executed; credited with the causal half, 0.5, as "
+                   f"the GPU figure); 1 warm-up head, then the median of 3 samples (this one: "
+                   f"{heads} heads in {elapsed:.1f} s)"),
     }
 
 
@@ -451,10 +630,12 @@ def main():
 
     components = {}
     result = {}
+    verifier = Verifier()
     if args.only in ("all", "fa"):
         B, H, S, D = 4, 32, 4096, 128
         wall_ms, kernels = bench_attention(core, ops, B, H, S, D, True, args.steps, args.warmup,
-                                           args.sample_ms)
+                                           args.sample_ms, verifier=verifier,
+                                           case="fa2_bf16_config5", check_heads=(0, 45, 90, 127))
         f_fwd = attention_flops(B * H, S, D, True)
         f_bwd = attention_flops(B * H, S, D, True, backward=True)
         fwd_ms = kernels["attn_fwd"]["ms"]
@@ -492,7 +673,8 @@ def main():
 
         # config 4: forward only, B8 H16 S1024 D64 non-causal.
         _, k4 = bench_attention(core, ops, 8, 16, 1024, 64, False, 0, args.warmup,
-                                args.sample_ms, backward=False)
+                                args.sample_ms, backward=False, verifier=verifier,
+                                case="fa2_fwd_bf16_config4", check_heads=(0, 77, 127))
         f4 = attention_flops(8 * 16, 1024, 64, False)
         ms4 = k4["attn_fwd"]["ms"]
         components["fa2_fwd_config4"] = {"tflops": round(f4 / (ms4 * 1e-3) / 1e12, 2),
@@ -500,36 +682,18 @@ def main():
                                          "ms": round(ms4, 4), "variant": k4["attn_fwd"]["variant"]}
         # the opt-in single-pass backward (bwd=atomic) at config 5, beside the split one
         _, ka = bench_attention(core, ops, B, H, S, D, True, 0, args.warmup, args.sample_ms,
-                                bwd="atomic")
+                                bwd="atomic", verifier=verifier, case="fa2_bf16_config5_atomic",
+                                check_heads=(3, 126))
         ms_a = ka["attn_bwd_preprocess"]["ms"] + ka["attn_bwd_fused"]["ms"]
         components["fa2_bwd_atomic"] = {
             "tflops": round(f_bwd / (ms_a * 1e-3) / 1e12, 2),
             "frac_of_peak": round(f_bwd / (ms_a * 1e-3) / 1e12 / 2500, 4),
             "ms": round(ms_a, 4), "fused_ms": round(ka["attn_bwd_fused"]["ms"], 4),
             "vs_split": round(bwd_ms / ms_a, 3), "variant": ka["attn_bwd_fused"]["variant"]}
-        # the deterministic one-call backward (bwd=stash: dK/dV kernel keeps dS
-        # for a dQ kernel, no recomputation), beside the split as well
-        _, ks = bench_attention(core, ops, B, H, S, D, True, 0, args.warmup, args.sample_ms,
-                                bwd="stash")
-        ms_s = ks["attn_bwd_preprocess"]["ms"] + ks["attn_bwd_fused"]["ms"]
-        components["fa2_bwd_stash"] = {
-            "tflops": round(f_bwd / (ms_s * 1e-3) / 1e12, 2),
-            "frac_of_peak": round(f_bwd / (ms_s * 1e-3) / 1e12 / 2500, 4),
-            "ms": round(ms_s, 4), "fused_ms": round(ks["attn_bwd_fused"]["ms"], 4),
-            "vs_split": round(bwd_ms / ms_s, 3), "variant": ks["attn_bwd_fused"]["variant"]}
-        # the split's two kernels in one grid (bwd=merged: dQ workgroups fill the
-        # dK/dV tail; bit-identical to the split), beside the split as well
-        _, km = bench_attention(core, ops, B, H, S, D, True, 0, args.warmup, args.sample_ms,
-                                bwd="merged")
-        ms_m = km["attn_bwd_preprocess"]["ms"] + km["attn_bwd_fused"]["ms"]
-        components["fa2_bwd_merged"] = {
-            "tflops": round(f_bwd / (ms_m * 1e-3) / 1e12, 2),
-            "frac_of_peak": round(f_bwd / (ms_m * 1e-3) / 1e12 / 2500, 4),
-            "ms": round(ms_m, 4), "fused_ms": round(km["attn_bwd_fused"]["ms"], 4),
-            "vs_split": round(bwd_ms / ms_m, 3), "variant": km["attn_bwd_fused"]["variant"]}
         # fp16 variant of config 5 (the reference's own attention element type)
         _, k16 = bench_attention(core, ops, B, H, S, D, True, 0, args.warmup, args.sample_ms,
-                                 element="f16")
+                                 element="f16", verifier=verifier, case="fa2_f16_config5",
+                                 check_heads=(1, 100))
         ms_f = k16["attn_fwd"]["ms"]
         ms_b = sum(k16[n]["ms"] for n in ("attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv"))
         components["fa2_f16_config5"] = {
@@ -543,7 +707,8 @@ def main():
         # any fp32 caller reaches.
         ref = {}
         for n in (1024, 2048, 4096):
-            ms, variant = bench_gemm(core, ops, n, 2, args.sample_ms, element="f32")
+            ms, variant = bench_gemm(core, ops, n, 2, args.sample_ms, element="f32",
+                                     verifier=verifier, case=f"gemm_f32_{n}")
             ref[f"gemm_f32_{n}"] = {"tflops": round(gemm_flops(n, n, n) / (ms * 1e-3) / 1e12, 2),
                                     "ms": round(ms, 4), "variant": variant}
         # fp32 at three shapes, f16 at the two the reference also publishes in f16
@@ -551,7 +716,8 @@ def main():
         for element, heads, seq in (("f32", 8, 512), ("f32", 8, 1024), ("f32", 16, 2048),
                                     ("f16", 8, 512), ("f16", 8, 1024)):
             _, kr = bench_attention(core, ops, 1, heads, seq, 64, False, 0, 2, args.sample_ms,
-                                    element=element)
+                                    element=element, verifier=verifier,
+                                    case=f"fa2_{element}_h{heads}_s{seq}_d64", check_heads=(0, heads - 1))
             ms_f = kr["attn_fwd"]["ms"]
             ms_b = sum(kr[k]["ms"] for k in ("attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv"))
             ref[f"fa2_{element}_h{heads}_s{seq}_d64"] = {
@@ -565,12 +731,14 @@ def main():
         components["reference_shapes_f32"] = ref
     if args.only in ("all", "gemm"):
         n = 8192
-        ms, variant = bench_gemm(core, ops, n, args.warmup, args.sample_ms)
+        ms, variant = bench_gemm(core, ops, n, args.warmup, args.sample_ms, verifier=verifier,
+                                 case="gemm_bf16_8192_config3")
         tf = gemm_flops(n, n, n) / (ms * 1e-3) / 1e12
         components["gemm_bf16_8192"] = {"tflops": round(tf, 2),
                                         "frac_of_peak": round(tf / 2500, 4),
                                         "ms": round(ms, 4), "variant": variant}
-        ms16, variant16 = bench_gemm(core, ops, n, args.warmup, args.sample_ms, element="f16")
+        ms16, variant16 = bench_gemm(core, ops, n, args.warmup, args.sample_ms, element="f16",
+                                     verifier=verifier, case="gemm_f16_8192")
         tf16 = gemm_flops(n, n, n) / (ms16 * 1e-3) / 1e12
         components["gemm_f16_8192"] = {"tflops": round(tf16, 2),
                                        "frac_of_peak": round(tf16 / 2500, 4),
@@ -579,14 +747,15 @@ def main():
         # B or A passed transposed).
         more = {}
         for n2, layout in ((1024, "nn"), (2048, "nn"), (4096, "nn"), (8192, "nt"), (8192, "tn")):
-            ms2, variant2 = bench_gemm(core, ops, n2, 2, args.sample_ms, layout=layout)
+            ms2, variant2 = bench_gemm(core, ops, n2, 2, args.sample_ms, layout=layout,
+                                       verifier=verifier, case=f"gemm_bf16_{layout}_{n2}")
             more[f"{layout}_{n2}"] = {"tflops": round(gemm_flops(n2, n2, n2) / (ms2 * 1e-3) / 1e12, 2),
                                       "ms": round(ms2, 4), "variant": variant2}
         components["gemm_bf16_sizes_and_layouts"] = more
         # The fused SAE encoder at an 8x dictionary over 8192 tokens of width 2048.
         rows, model, features = 8192, 2048, 16384
         ms_s, variant_s = bench_sae(core, ops, rows, model, features, args.warmup,
-                                    args.sample_ms)
+                                    args.sample_ms, verifier=verifier, case="sae_encode_bf16")
         tf_s = gemm_flops(rows, features, model) / (ms_s * 1e-3) / 1e12
         components["sae_encode_bf16_8192x2048x16384"] = {
             "tflops": round(tf_s, 2), "frac_of_peak": round(tf_s / 2500, 4),
@@ -598,6 +767,12 @@ def main():
                                     "frac": round(tf / 2500, 4),
                                     "traffic": measured_traffic(variant)})
 
+    if verifier.failures:
+        print("bench.py: results failed verification, no figure reported:\n  "
+              + "\n  ".join(verifier.failures), file=sys.stderr, flush=True)
+        print(json.dumps({"verified": {"ok": False, "failures": verifier.failures,
+                                       "cases": verifier.record}}), file=sys.stderr, flush=True)
+        sys.exit(1)
     line = {
         "metric": METRIC,
         "value": result.get("value"),
@@ -618,6 +793,7 @@ def main():
                    "k": 8192, "parallelism": "none (1 GPU)"},
         "roofline": result.get("roofline"),
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
+        "verified": {"ok": not verifier.failures, "cases": verifier.record},
         "components": components,
         "device": core.device_name(),
     }

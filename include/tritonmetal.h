@@ -18,23 +18,24 @@
  *       * a gfx950 code object image (tm_load_metallib),
  *       * HIP C++ source compiled at run time by hiprtc (tm_compile_msl), or
  *       * a built-in library spec "builtin [element=f32|f16|bf16]
- *         [head_dim=N] [causal=0|1] [bwd=split|atomic|stash|merged]" (tm_compile_msl),
+ *         [head_dim=N] [causal=0|1] [bwd=split|atomic]" (tm_compile_msl),
  *         which names the library's hand-written gfx950 kernels for the dense
  *         hot path: matmul_kernel, attn_fwd, attn_bwd_preprocess, attn_bwd_dq,
  *         attn_bwd_dkdv, sae_encode_kernel (relu(x @ W + b),
  *         Sources/TritonMetalMLX/SAEEncoder.swift:29-40), tm_probe, and with
- *         bwd=atomic, bwd=stash or bwd=merged attn_bwd_fused (the backward in one call
+ *         bwd=atomic attn_bwd_fused (the backward in one call
  *         that AttentionBackwardKernel.swift:27-41 names: Q, K, V, dO, dQ, dK,
  *         dV, L, Delta, sm_scale, stride_head, stride_seq, stride_lse, n_ctx;
- *         atomic sums dQ with fp32 atomics, stash keeps dS for a dQ pass,
- *         merged runs the split's dK/dV and dQ kernels in one grid).
+ *         dQ summed with fp32 atomics).
  *   - a "buffer" is device memory in HBM (hipMalloc).  tm_buffer_contents
  *     gives it a host-addressable mirror (pinned host memory) that stands in
  *     for the reference's unified memory: while the mirror exists, host
  *     writes through it reach the kernels of later launches and the results
  *     of a launch are in it when the launch returns (a launch that binds such
  *     a buffer copies it to HBM before the dispatch and back afterwards, and
- *     waits).  Buffers never mapped this way are not copied.
+ *     waits: the full buffer both ways, and tm_launch_async waits too).
+ *     Buffers never mapped this way, or unmapped by tm_buffer_unmap, are not
+ *     copied.
  *   - launches run on one library-owned HIP stream.
  */
 #ifndef TRITONMETAL_H
@@ -148,8 +149,8 @@ int32_t tm_launch_timed(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int6
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  A dispatch that needs a work buffer
  * (attn_bwd_fused's fp32 dQ accumulator under bwd=atomic, heads * n_ctx *
- * head_dim * 4 bytes, or its dS stash under bwd=stash, about heads * n_ctx^2 * 2)
- * takes it from a static device array of 64 MiB per device, held from the
+ * head_dim * 4 bytes, or the partial sums of a split GEMM or generic attention
+ * kernel) takes it from a static device array of 64 MiB per device, held from the
  * first such call until the process ends; larger requests are refused with an
  * error (use tm_launch).  The caller passes inputs and outputs as for
  * tm_launch; this call waits.  Calls in one process are serialised on a lock;
@@ -157,6 +158,13 @@ int32_t tm_launch_timed(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int6
  * needs zeroed.  0 / -1. */
 int32_t tm_launch_noalloc(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads,
                           const int32_t *kinds, const int64_t *values, int32_t argc);
+/* Drop the host mirror that tm_buffer_contents made: host writes made through
+ * it are copied to HBM, the pinned memory is freed, and the address it gave
+ * is no longer valid.  Launches that bind the buffer stop copying it and no
+ * longer wait (tm_launch_async is asynchronous again).  A later
+ * tm_buffer_contents makes a new mirror.  No-op without a mirror.  0 / -1.
+ * No reference counterpart (the reference's buffers are unified memory). */
+int32_t tm_buffer_unmap(int64_t buffer);
 /* Name of the device function the last planned dispatch of `kernel` ran (the
  * symbol rocprof reports), NULL on failure.  For tests and profiling. */
 char *tm_kernel_variant(int64_t kernel);

@@ -29,7 +29,7 @@ def test_library_is_the_in_tree_build(core):
 
 def test_every_declared_export_is_present(core):
     names = declared_exports()
-    assert len(names) == 28
+    assert len(names) == 29
     for name in names:
         assert hasattr(core._lib, name), name
     # The reference's 23 exports are all declared.
@@ -124,8 +124,6 @@ def test_builtin_spec_round_trips_through_emit(core):
         "builtin element=bf16 head_dim=64 causal=0"
     assert core.emit_msl("builtin element=bf16 head_dim=128 bwd=atomic") == \
         "builtin element=bf16 head_dim=128 causal=0 bwd=atomic"
-    assert core.emit_msl("builtin element=f16 bwd=stash causal=1") == \
-        "builtin element=f16 head_dim=64 causal=1 bwd=stash"
 
 
 @pytest.mark.parametrize("spec,message", [
@@ -133,7 +131,8 @@ def test_builtin_spec_round_trips_through_emit(core):
     ("builtin head_dim=0", "head_dim must be an integer in 1..128"),
     ("builtin head_dim=129", "head_dim must be an integer in 1..128"),
     ("builtin causal=2", "causal must be 0 or 1"),
-    ("builtin bwd=fast", "bwd must be split, atomic, stash or merged"),
+    ("builtin bwd=fast", "bwd must be split or atomic"),
+    ("builtin bwd=stash", "bwd must be split or atomic"),
     ("builtin colour=red", "unknown key 'colour'"),
     ("builtin element", "expected key=value"),
 ])
@@ -162,11 +161,9 @@ def test_kernel_info_publishes_every_builtin(core):
         assert k["threads_per_threadgroup"] > 0 and k["block_size"] > 0
 
 
-def test_fused_backward_is_offered_only_with_bwd_atomic_or_stash(core):
+def test_fused_backward_is_offered_only_with_bwd_atomic(core):
     split = json.loads(core.kernel_info("builtin element=bf16 head_dim=128 causal=1"))
     assert "attn_bwd_fused" not in {k["name"] for k in split["kernels"]}
-    stash = json.loads(core.kernel_info("builtin element=bf16 head_dim=128 causal=1 bwd=stash"))
-    assert "attn_bwd_fused" in {k["name"] for k in stash["kernels"]}
     info = json.loads(core.kernel_info("builtin element=bf16 head_dim=128 causal=1 bwd=atomic"))
     fused = {k["name"]: k for k in info["kernels"]}["attn_bwd_fused"]
     # Q, K, V, dO, dQ, dK, dV, L, Delta, sm_scale, stride_head, stride_seq,

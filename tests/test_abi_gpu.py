@@ -161,6 +161,34 @@ def test_buffer_contents_is_a_host_view(core, device):
         core.release_library(library)
 
 
+def test_unmap_drops_the_host_mirror(core, device):
+    """tm_buffer_unmap copies host writes made through the mirror down to HBM,
+    frees it, and later launches work on HBM alone; a second
+    tm_buffer_contents makes a fresh mirror of the current contents."""
+    src = _upload(core, [float(i) for i in range(64)])
+    dst = core.alloc_buffer(256)
+    library = core.compile_msl(COPY)
+    kernel = core.load_kernel(library, "copy_kernel")
+    try:
+        view = _host_view(core, src, 64)
+        view[5] = -7.0                           # written through the mirror only
+        assert core._lib.tm_buffer_unmap(src) == 0
+        assert core._lib.tm_buffer_unmap(src) == 0   # no mirror: no-op
+        core.launch(kernel, (1, 1, 1), 64, [core.ARG_BUFFER] * 2, [src, dst])
+        want = [float(i) for i in range(64)]
+        want[5] = -7.0
+        assert list(_download(core, dst, 64)) == want
+        assert list(_host_view(core, src, 64)) == want
+        assert core._lib.tm_buffer_unmap(src) == 0
+        assert core._lib.tm_buffer_unmap(0) == -1
+        assert "is not live" in core.last_error()
+    finally:
+        core.free_buffer(src)
+        core.free_buffer(dst)
+        core.release_kernel(kernel)
+        core.release_library(library)
+
+
 def test_host_view_of_a_kernel_output_mapped_after_the_launch(core, device):
     src = _upload(core, [float(i) for i in range(64)])
     dst = core.alloc_buffer(256)
@@ -342,6 +370,59 @@ def test_concurrent_launches_from_several_threads(core, device):
         t.join()
     assert errors == []
     assert core.live_handle_count() == live
+
+
+def test_concurrent_workspace_launches_from_several_threads(core, device):
+    """Threads sharing one library launch GEMMs that take the K-split path
+    (fp32 partials in the library workspace, then a reduce dispatch) with
+    sizes that grow the workspace while other threads' sequences are queued
+    (tm_launch_async, one wait at the end).  Each launch plans and queues its
+    whole sequence under the library's launch lock, so no sequence binds a
+    freed workspace or sums another thread's partials."""
+    import threading
+
+    from triton_metal import ops
+    from triton_metal.buffer import DeviceBuffer
+    kernel = ops.library("bf16").kernels["matmul_kernel"]
+    errors = []
+    barrier = threading.Barrier(4)
+
+    def worker(seed):
+        try:
+            rng = np.random.default_rng(100 + seed)
+            # a few rows against a long K: the planner splits K across workgroups
+            m, n, k = 64, 1024 + 256 * seed, 4096 + 2048 * seed
+            a = rng.standard_normal((m, k), dtype=np.float32)
+            b = rng.standard_normal((k, n), dtype=np.float32)
+            A = DeviceBuffer.from_numpy(a, "bfloat16")
+            B = DeviceBuffer.from_numpy(b, "bfloat16")
+            outs = [DeviceBuffer((m, n), "bfloat16") for _ in range(4)]
+            try:
+                a, b = A.float32(), B.float32()
+                want = a.astype(np.float64) @ b.astype(np.float64)
+                barrier.wait()
+                for C in outs:
+                    grid, kinds, values = ops.matmul_args(A, B, C, m, n, k)
+                    core.launch_async(kernel, grid, 128, kinds, values)
+                core.synchronize()
+                for C in outs:
+                    got = C.float32()
+                    err = np.max(np.abs(got - want) / np.maximum(1.0, np.abs(want)))
+                    if err > 2e-2:
+                        errors.append((seed, float(err)))
+            finally:
+                for x in (A, B, *outs):
+                    x.free()
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append((seed, repr(e)))
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert errors == []
+    assert "K ranges" in core.kernel_variant(kernel)
 
 
 BLOCK_KERNEL = r"""

@@ -1,21 +1,15 @@
-"""The opt-in backward in one call (kernel attn_bwd_fused), in its two forms:
-  bwd=atomic  dK and dV from the same arithmetic as attn_bwd_dkdv, dQ
-              accumulated across key blocks with fp32 atomics;
-  bwd=stash   the dK/dV kernel also writes the rounded dS it computes, and a
-              dQ kernel reads it back (no recomputation, deterministic);
-  bwd=merged  the split's dK/dV and dQ kernels in one grid (head_dim 128; at
-              64 the two kernels back to back): dQ, dK, dV bit-identical to
-              the split.
+"""The opt-in backward in one call (kernel attn_bwd_fused, bwd=atomic): dK
+and dV from the same arithmetic as attn_bwd_dkdv, dQ accumulated across key
+blocks with fp32 atomics.
 
 The reference chose the split backward for determinism and named the atomic
 form as the unmeasured alternative (AttentionBackwardKernel.swift:27-41,
 docs/COMPARISON.md:151-154); its backward tests set the bar used here
 (AttentionBackwardTests.swift: hybrid error against an fp64 oracle).
 
-Checks, for both forms: parity with the fp64 oracle at small and ragged
-shapes, dK/dV bit-identical to the split kernels (the same per-block
-arithmetic), dQ of two runs within one rounding unit of each other (atomic) or
-identical (stash), and, at the headline causal shape (B4 H32 S4096 D128) in
+Checks: parity with the fp64 oracle at small and ragged shapes, dK/dV
+bit-identical to the split kernels (the same per-block arithmetic), dQ of two
+runs within one rounding unit of each other, and, at the headline causal shape (B4 H32 S4096 D128) in
 full, dK/dV identical to and dQ within the parity tolerance of the split
 path."""
 
@@ -86,10 +80,7 @@ class _Run:
         _core.launch(kern, (1, self.heads, 1), 128, [B] * 9 + [F, I, I, I, I],
                      [self.h(x) for x in ("q", "k", "v", "do", "dq", "dk", "dv", "lse", "delta")] +
                      self.tail)
-        want = {"atomic": ("tm_attn_fused_fast_",), "stash": ("tm_attn_dkdv_stash_",),
-                # one merged grid at head_dim 128, the two split kernels at 64
-                "merged": ("tm_attn_bwd_merged_", "tm_attn_dkdv_fast_")}[self.bwd]
-        assert any(w in _core.kernel_variant(kern) for w in want)
+        assert "tm_attn_fused_fast_" in _core.kernel_variant(kern)
         return self.grads()
 
     def free(self):
@@ -97,7 +88,7 @@ class _Run:
             b.free()
 
 
-BWD = ["atomic", "stash", "merged"]
+BWD = ["atomic"]
 
 
 @pytest.mark.parametrize("bwd", BWD)
@@ -120,16 +111,13 @@ def test_fused_backward_matches_oracle(bwd, element, dim, causal, seq, device):
     # per-block arithmetic and accumulation order are the same
     assert np.array_equal(fused["dk"], split["dk"])
     assert np.array_equal(fused["dv"], split["dv"])
-    if bwd == "merged":
-        assert np.array_equal(fused["dq"], split["dq"])
 
 
 @pytest.mark.parametrize("bwd", BWD)
 def test_fused_backward_workspace_regrows_and_is_cleared(bwd, device):
     """One library, three problems in a row (small, larger, small): the
     library's workspace grows, and each launch starts from a clean state (a
-    stale atomic sum would double dQ; a stale stash would feed the previous
-    problem's dS)."""
+    stale atomic sum would double dQ)."""
     for seq, heads in ((100, 1), (700, 3), (100, 1)):
         run = _Run(heads, seq, 128, "bf16", True, seed=seq + heads, bwd=bwd)
         try:
@@ -143,8 +131,6 @@ def test_fused_backward_workspace_regrows_and_is_cleared(bwd, device):
         # the second launch sums the same partials in another order: one
         # rounding unit of the element type apart at most, not twice the value
         assert T.hybrid_error(again["dq"], fused["dq"]) <= 2 * T.U_BF16
-        if bwd in ("stash", "merged"):
-            assert np.array_equal(again["dq"], fused["dq"])
         assert np.array_equal(again["dk"], fused["dk"])
 
 
@@ -166,8 +152,6 @@ def test_fused_backward_config5_full_size_against_split(bwd, device):
     assert np.array_equal(fused["dk"], split["dk"])
     assert np.array_equal(fused["dv"], split["dv"])
     assert np.all(np.isfinite(fused["dq"]))
-    if bwd == "merged":
-        assert np.array_equal(fused["dq"], split["dq"])
     # the two dQ come from differently ordered MFMA sums of dS (itself
     # recomputed in the other orientation, so a rounded dS may differ by one
     # unit): the same hybrid metric the oracle tests use, against the split

@@ -77,10 +77,7 @@ def test_every_barrier_waits_for_the_waves_own_lds_copies():
             if not any(K.is_lds_dma(mn, ops) for _, mn, ops, _ in insns):
                 continue
             checked += 1
-            # the stash dQ kernel rotates three buffers: a copy may cross one
-            # barrier in flight
-            depth = 1 if name.startswith("tm_attn_dq_stash_") else 0
-            bad = K.barriers_with_copy_in_flight(insns, depth)
+            bad = K.barriers_with_copy_in_flight(insns, 0)
             assert not bad, f"{name}: s_barrier at {[hex(a) for a in bad]} with an LDS copy in flight"
     assert checked >= 40  # the specialised attention and GEMM kernels
 

@@ -193,6 +193,22 @@ def test_blas_head_restatement_matches_the_reference_numpy_and_fp64(causal):
         assert np.allclose(got, want[name][0], rtol=1e-4, atol=1e-5), name
 
 
+@pytest.mark.parametrize("block", [1, 7, 16, 40, 64])
+def test_blocked_causal_head_matches_the_masked_form_and_fp64(block):
+    # The CPU baseline's row-blocked causal form visits only visible keys; it
+    # must equal the masked full-square form (and the fp64 oracle) for every
+    # block size, including ragged last blocks and blocks of one row.
+    rng = np.random.default_rng(11)
+    q, k, v, d_out = (rng.standard_normal((1, 40, 16), dtype=np.float32) for _ in range(4))
+    scale = 0.25
+    got = R.attention_head_causal_blocked_f32(q[0], k[0], v[0], d_out[0], scale, block=block)
+    full = R.attention_head_f32(q[0], k[0], v[0], d_out[0], scale, causal=True)
+    want = R.attention_backward(q, k, v, d_out, scale, causal=True)
+    for g, f, name in zip(got, full, ("o", "dq", "dk", "dv")):
+        assert np.allclose(g, f, rtol=1e-4, atol=1e-5), name
+        assert np.allclose(g, want[name][0], rtol=1e-4, atol=1e-5), name
+
+
 def test_tolerance_metrics():
     assert T.hybrid_error([1.0, 10.0], [1.0, 11.0]) == pytest.approx(1 / 11)
     assert T.hybrid_error([0.5], [0.0]) == pytest.approx(0.5)

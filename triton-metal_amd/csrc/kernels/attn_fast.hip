@@ -875,17 +875,15 @@ TM_DEV void attn_dq_fast(const TmAttnDqArgs &p, char *lds, int wg, int nwg) {
  * are independent, so the wave's VALU work overlaps its MFMA work.  Buffer
  * indices are compile-time (PH = i mod 3) so the compiler sees that the
  * in-flight copy never aliases the tiles being read. */
-template <typename T, int D, bool CAUSAL, bool FUSED = false, bool STASH = false>
-TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, void *stash = nullptr,
-                           int stash_keys = 0, int stash_blocks = 0) {
+template <typename T, int D, bool CAUSAL, bool FUSED = false>
+TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr) {
   /* query rows per step: 64 at D = 64 (twice the MFMA work per barrier and
    * per softmax pass; measured 7% faster), 32 at D = 128, where 64 would not
    * fit the registers */
   constexpr int BN = 128, KW = 32, BM = D == 64 ? 64 : 32;
   /* The kernel carries -dS = P (Delta - dP): the dP MFMAs run on -V and start
    * from Delta, so no subtraction per element.  dK accumulates -dK and flips
-   * the sign at the store; FUSED adds dQ with -K, STASH stores -dS and its dQ
-   * pass flips the sign. */
+   * the sign at the store; FUSED adds dQ with -K. */
   constexpr int QT = BM / 16, KK = BM / 32;
   constexpr int KS = D / 32;
   constexpr int TILE = BM * D * 2;
@@ -1113,33 +1111,6 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
       }
   };
 
-  /* STASH: dS^T of block `blk` into this head's stash, laid out as
-   * [query block of 32][stash_keys][32] (stash_index): a lane's B operand of
-   * one key (8 queries, rounded) is one 16-byte store, and a wave's store
-   * instruction writes 16 keys x 64 bytes, 1 KB contiguous, through a buffer
-   * resource over the head's stash (lane offsets fixed, the block's in an
-   * SGPR).  Keys past n
-   * hold the finite dS of the clamped K and V rows (the dQ pass multiplies
-   * them by zero K rows); queries past n hold the masked zeros. */
-  const int64_t stash_head = (int64_t)stash_blocks * stash_keys * 32; /* elements */
-  int stash_off[2] = {0, 0};
-  if constexpr (STASH) {
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) stash_off[kt] = (kw0 + kt * 16 + c) * 64 + 16 * g;
-  }
-  auto put_stash = [&](int blk, const u32x4 (&dsv)[2][KK]) {
-    const __amdgpu_buffer_rsrc_t stash_rs = __builtin_amdgcn_make_buffer_rsrc(
-        (T *)stash + (int64_t)bh * stash_head, (short)0, (int)(stash_head * 2), 0x00020000);
-    const int sblk = (q_start + blk * BM) / 32;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      const int soff = (sblk + kk) * stash_keys * 64;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-        __builtin_amdgcn_raw_buffer_store_b128(dsv[kt][kk], stash_rs, stash_off[kt], soff, 0);
-    }
-  };
-
   char *const bufs[3] = {lds_0, lds_1, lds_2};
   u32x4 pf[2][KK], dsf[2][KK]; /* P and dS of the block whose gradients are pending */
 
@@ -1159,10 +1130,6 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
     }
     grads(cur, pf, dsf);
     if constexpr (FUSED) dq_block(i);
-    /* block i's dS, stored after the step's copies: the wait below lets
-     * these last 2 KK stores stay in flight (vmcnt counts in issue order), so
-     * they complete during the next step instead of stalling this one */
-    if constexpr (STASH) put_stash(i, dsf);
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -1170,17 +1137,8 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
         pf[kt][kk] = pf2[kt][kk];
         dsf[kt][kk] = ds2[kt][kk];
       }
-    if constexpr (STASH) {
-      /* a barrier ordering LDS only: __syncthreads' workgroup fence would
-       * also wait for the stash stores, every step */
-      __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * KK)); /* vmcnt(2 KK): the copies */
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-      __builtin_amdgcn_s_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-    } else {
-      wait_vmem();
-      __syncthreads();
-    }
+    wait_vmem();
+    __syncthreads();
   };
   using Interior = std::integral_constant<bool, false>;
   using Edge = std::integral_constant<bool, true>;
@@ -1254,187 +1212,6 @@ TM_DEV void attn_dkdv_fast(const TmAttnDkdvArgs &p, float *dq_acc = nullptr, voi
 }
 
 
-/* Position of query q (0..31) in a 32-query stash row: the groups of 4
- * queries come in the order 0, 4, 1, 5, 2, 6, 3, 7, the order in which a
- * dK/dV lane holds them (4g .. 4g+3, then 16 + 4g .. +3). */
-TM_DEV int stash_pos(int q) {
-  const int qg = q >> 2;
-  return 4 * (qg < 4 ? 2 * qg : 2 * (qg - 4) + 1) + (q & 3);
-}
-
-/* ---- backward: dQ from a dS stash (bwd=stash) ----------------------------
- * dQ = dS K without recomputing S and dP: the dK/dV kernel's stash form wrote
- * -dS^T (rounded to the element type, as the split dq kernel rounds dS before
- * its dot; the sign is flipped at the store) as [query block of 32][stash_keys][32 queries in stash_pos order].
- * One workgroup = 8 waves = 256 queries (one workgroup per CU), the key
- * blocks (64 keys) of its head up to the last one its queries see; per block
- * the K tile and a [64 keys][256 queries] dS^T tile (two halves of 128,
- * gathered from 8 query blocks) are copied to LDS, three blocks in rotation so
- * that two blocks' copies are in flight while one is computed, and
- *   dQ^T += K^T dS^T   (both operands by ds_read_b64_tr_b16).
- * The stream is HBM-bound: it reads the heads * n_ctx^2 / 2 stash once. */
-template <typename T, int D, bool CAUSAL>
-TM_DEV void attn_dq_stash(const TmAttnFusedArgs &a) {
-  const TmAttnDkdvArgs &p = a.kv;
-  constexpr int NW = 8, QW = 32, BM = NW * QW, BN = 64;
-  constexpr int KT = BN * D * 2;        /* K tile */
-  constexpr int HT = BN * 128 * 2;      /* one half of the dS^T tile: 64 rows of 128 queries */
-  constexpr int BUF = KT + 2 * HT;
-  __shared__ __align__(1024) char lds_0[BUF];
-  __shared__ __align__(1024) char lds_1[BUF];
-  __shared__ __align__(1024) char lds_2[BUF];
-
-  typedef typename Vec8<T>::type v8;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 4, c = lane & 15;
-  const int n = p.n_ctx;
-  const int nqb = (n + BM - 1) / BM;
-  const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  int bh, qb;
-  if (CAUSAL) {
-    causal_order(logical, nqb, p.heads, bh, qb);
-    qb = nqb - 1 - qb;
-  } else {
-    bh = logical / nqb;
-    qb = logical - bh * nqb;
-  }
-  const int q0 = qb * BM;
-  const int qw0 = q0 + wave * QW;
-  const int half = wave >> 2;           /* which 128-query half of the dS tile */
-  const int64_t ss = p.stride_seq;
-  const T *Kg = (const T *)p.k + (int64_t)bh * p.stride_head;
-  T *dQg = (T *)a.dq + (int64_t)bh * p.stride_head;
-  const int kp = a.stash_keys;
-
-  /* K rows through a resource clipped at n; this wave's KPW 1 KB pieces */
-  const u32x4 krs = raw_buffer_rsrc(Kg, ((int64_t)(n - 1) * ss + D) * 2);
-  constexpr int KCPR = D / 8, KRPI = 64 / KCPR, KPW = KT / 1024 / NW;
-  static_assert(KPW * 1024 * NW == KT, "K tile pieces");
-  int koff[KPW];
-#pragma unroll
-  for (int i = 0; i < KPW; ++i) {
-    const int t = wave * KPW + i;
-    const int row = t * KRPI + lane / KCPR;
-    koff[i] = row * (int)ss * 2 + (((lane % KCPR) ^ swz<D>(row)) << 4);
-  }
-  /* the head's stash; this wave's four 1 KB pieces of the two dS^T halves */
-  const u32x4 srs = raw_buffer_rsrc((const T *)a.stash + (int64_t)bh * a.stash_blocks * kp * 32,
-                                    (int64_t)a.stash_blocks * kp * 64);
-  int soff[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = wave * 4 + i, h = t >> 4, row = (t & 15) * 4 + lane / 16;
-    const int chunk = (lane % 16) ^ swz<128>(row);
-    soff[i] = ((q0 / 32 + 4 * h + (chunk >> 2)) * kp + row) * 64 + (chunk & 3) * 16;
-  }
-
-  const int kend = CAUSAL ? min(n, q0 + BM) : n;
-  const int nblocks = (kend + BN - 1) / BN;
-  /* KPW + 4 copies per wave per block, the count the waits below leave in
-   * flight.
-   * Every step issues them, also past the last block (rows out of the
-   * resources' range arrive as zeros into a buffer no step reads), so the
-   * wait is the same on every path. */
-  auto stage = [&](char *buf, int j) {
-    const int rows = j * BN;
-#pragma unroll
-    for (int i = 0; i < KPW; ++i)
-      lds_copy16_buffer(krs, koff[i] + rows * (int)ss * 2, lds_addr(buf + (wave * KPW + i) * 1024));
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      lds_copy16_buffer(srs, soff[i] + rows * 64, lds_addr(buf + KT + (wave * 4 + i) * 1024));
-  };
-  /* a barrier ordering LDS only, after this wave's copies of the next block
-   * have landed (the copies of the block after it stay in flight) */
-  auto sync = [&]() {
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (KPW + 4)); /* vmcnt(KPW + 4) */
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-  };
-  /* B operand of query tile col0 .. +15 of this wave's half: k = 8 keys
-   * from rows 32 kk, columns in stash_pos order */
-  auto ds_operand = [&](const char *tile, int kk, int col0) {
-    const int q = col0 + 4 * (c & 3);
-    const int pos = (q & ~31) + stash_pos(q & 31);
-    const int ra = 32 * kk + 4 * g + (c >> 2);
-    const int chunk = pos >> 3, hf = (pos >> 2) & 1;
-    const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) s16x4 *)(tile + tile_off<128>(ra, chunk) + (hf << 3)));
-    const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) s16x4 *)(tile + tile_off<128>(ra + 16, chunk) + (hf << 3)));
-    const u32x2 ux = __builtin_bit_cast(u32x2, x), uy = __builtin_bit_cast(u32x2, y);
-    return (u32x4){ux[0], ux[1], uy[0], uy[1]};
-  };
-  f32x4 acc[D / 16][2];
-#pragma unroll
-  for (int dt = 0; dt < D / 16; ++dt) acc[dt][0] = acc[dt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  /* causal: a wave's half sees keys below q0 + 128 (half + 1) only; the
-   * stash holds no values above that diagonal for the first half (the dK/dV
-   * walk of those keys starts at q0 + 128) */
-  const int key_end = CAUSAL ? q0 + 128 * (half + 1) : n;
-  auto step = [&](const char *cur, int j) {
-    if (CAUSAL && j * BN >= key_end) return;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      u32x4 sb[2];
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
-        sb[qt] = ds_operand(cur + KT + half * HT, kk, (wave & 3) * QW + qt * 16);
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) {
-        const v8 ka = as_vec8<T>(read_kmajor_operand<D>(cur, 32 * kk, dt * 16, g, c));
-        acc[dt][0] = mfma_16x16x32(ka, as_vec8<T>(sb[0]), acc[dt][0]);
-        acc[dt][1] = mfma_16x16x32(ka, as_vec8<T>(sb[1]), acc[dt][1]);
-      }
-    }
-  };
-
-  stage(lds_0, 0);
-  stage(lds_1, 1);
-  sync();
-  int j = 0;
-  for (; j + 3 <= nblocks; j += 3) {
-    /* phases 0, 1, 2: compute from lds_{j%3}, copy block j+2 into the one
-     * read a step ago */
-    stage(lds_2, j + 2);
-    step(lds_0, j);
-    sync();
-    stage(lds_0, j + 3);
-    step(lds_1, j + 1);
-    sync();
-    stage(lds_1, j + 4);
-    step(lds_2, j + 2);
-    sync();
-  }
-  for (; j < nblocks; ++j) {
-    char *cur = j % 3 == 0 ? lds_0 : j % 3 == 1 ? lds_1 : lds_2;
-    char *far = j % 3 == 0 ? lds_2 : j % 3 == 1 ? lds_0 : lds_1;
-    stage(far, j + 2);
-    step(cur, j);
-    sync();
-  }
-  /* the copies past the last block must land before the LDS is released */
-  wait_vmem();
-
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int qi = qw0 + qt * 16 + c;
-    if (qi < n) {
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) {
-        u32x2 w;
-        /* the stash holds -dS */
-        w[0] = pack2<T>(acc[dt][qt][0] * -p.sm_scale, acc[dt][qt][1] * -p.sm_scale);
-        w[1] = pack2<T>(acc[dt][qt][2] * -p.sm_scale, acc[dt][qt][3] * -p.sm_scale);
-        *(u32x2 *)(dQg + (int64_t)qi * ss + dt * 16 + 4 * g) = w;
-      }
-    }
-  }
-}
-
 /* ---- backward: dK, dV at two waves per SIMD -------------------------------
  * The same work split as attn_dkdv_fast (a workgroup of 4 waves owns 128 keys,
  * a wave 32 of them, and walks 32-query blocks), built for two waves per SIMD
@@ -1452,7 +1229,7 @@ TM_DEV void attn_dq_stash(const TmAttnFusedArgs &a) {
  * As in attn_dkdv_fast, the dP MFMAs run on -V (negated once in LDS) and
  * start from Delta, so they deliver Delta - dP, and the kernel carries
  * -dS = P (Delta - dP) with one multiply; the arithmetic is the same as that
- * kernel's (and its fused and stash forms'), so dK and dV are bit-identical. */
+ * kernel's (and its fused form's), so dK and dV are bit-identical. */
 struct Dkdv2wLds { static constexpr int BYTES = 128 * 128 * 2 + 2 * (2 * 32 * 128 * 2 + 32 * 8); };
 template <typename T, int D, bool CAUSAL>
 TM_DEV void attn_dkdv_2w(const TmAttnDkdvArgs &p, char *lds, int wg, int nwg) {
@@ -1673,39 +1450,6 @@ TM_DEV void attn_dkdv_2w(const TmAttnDkdvArgs &p, char *lds, int wg, int nwg) {
   tm_attn_dkdv_fast_##TN##_d128##CN(TmAttnDkdvArgs p) {                                       \
     __shared__ __align__(1024) char lds[Dkdv2wLds::BYTES];                                    \
     attn_dkdv_2w<T, 128, CAUSAL>(p, lds, blockIdx.x, gridDim.x);                              \
-  }                                                                                           \
-  /* bwd=merged: one grid, the dK/dV workgroups first (the heavier ones), then    \
-   * the dQ workgroups, each running the split kernels' code over one LDS array  \
-   * (the larger of the two), so dQ work fills the dK/dV tail and the results    \
-   * are bit-identical to the split's.  The dQ part's xcd_remap assumes the     \
-   * dK/dV part's workgroup count is a multiple of 8 (otherwise only the L2     \
-   * locality of its mapping changes). */                                        \
-  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void  \
-  tm_attn_bwd_merged_##TN##_d128##CN(TmAttnFusedArgs a) {                                     \
-    constexpr int BYTES =                                                                     \
-        Dkdv2wLds::BYTES > DqLds<128>::BYTES ? Dkdv2wLds::BYTES : DqLds<128>::BYTES;          \
-    __shared__ __align__(1024) char lds[BYTES];                                               \
-    const int nkv = (int)gridDim.x / 2;                                                       \
-    if ((int)blockIdx.x < nkv) {                                                              \
-      attn_dkdv_2w<T, 128, CAUSAL>(a.kv, lds, blockIdx.x, nkv);                               \
-    } else {                                                                                  \
-      TmAttnDqArgs q{};                                                                       \
-      q.q = a.kv.q;                                                                           \
-      q.k = a.kv.k;                                                                           \
-      q.v = a.kv.v;                                                                           \
-      q.dout = a.kv.dout;                                                                     \
-      q.dq = a.dq;                                                                            \
-      q.lse = a.kv.lse;                                                                       \
-      q.delta = a.kv.delta;                                                                   \
-      q.sm_scale = a.kv.sm_scale;                                                             \
-      q.stride_head = a.kv.stride_head;                                                       \
-      q.stride_seq = a.kv.stride_seq;                                                         \
-      q.stride_lse = a.kv.stride_lse;                                                         \
-      q.n_ctx = a.kv.n_ctx;                                                                   \
-      q.head_dim = a.kv.head_dim;                                                             \
-      q.heads = a.kv.heads;                                                                   \
-      attn_dq_fast<T, 128, CAUSAL>(q, lds, blockIdx.x - nkv, (int)gridDim.x - nkv);           \
-    }                                                                                         \
   }
 #define TM_DKDV_FAST_64(T, TN, CAUSAL, CN)                                                    \
   extern "C" __global__ __launch_bounds__(256) void tm_attn_dkdv_fast_##TN##_d64##CN(         \
@@ -1719,22 +1463,7 @@ TM_DEV void attn_dkdv_2w(const TmAttnDkdvArgs &p, char *lds, int wg, int nwg) {
       TmAttnFusedArgs p) {                                                                    \
     attn_dkdv_fast<T, D, CAUSAL, true>(p.kv, p.dq_acc);                                       \
   }
-/* ... and the stash form (bwd=stash): dK, dV, and dS^T written for a dQ pass */
-#define TM_BWD_STASH(T, TN, D, CAUSAL, CN)                                                    \
-  extern "C" __global__ __launch_bounds__(256) void tm_attn_dkdv_stash_##TN##_d##D##CN(       \
-      TmAttnFusedArgs p) {                                                                    \
-    attn_dkdv_fast<T, D, CAUSAL, false, true>(p.kv, nullptr, p.stash, p.stash_keys,            \
-                                              p.stash_blocks);                                \
-  }                                                                                           \
-  extern "C" __global__ __launch_bounds__(512) void tm_attn_dq_stash_##TN##_d##D##CN(          \
-      TmAttnFusedArgs p) {                                                                    \
-    attn_dq_stash<T, D, CAUSAL>(p);                                                           \
-  }
 #define TM_BWD_FAST_ALL(T, TN)           \
-  TM_BWD_STASH(T, TN, 64, false, )       \
-  TM_BWD_STASH(T, TN, 64, true, _causal) \
-  TM_BWD_STASH(T, TN, 128, false, )      \
-  TM_BWD_STASH(T, TN, 128, true, _causal) \
   TM_BWD_FUSED(T, TN, 64, false, )       \
   TM_BWD_FUSED(T, TN, 64, true, _causal) \
   TM_BWD_FUSED(T, TN, 128, false, )      \

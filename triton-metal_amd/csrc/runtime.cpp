@@ -218,24 +218,16 @@ struct BuiltinSpec {
   Element element = Element::F32;
   int head_dim = 64;
   bool causal = false;
-  /* bwd=atomic or bwd=stash: the library also offers attn_bwd_fused, a
-   * backward in one call.  atomic: one dK/dV/dQ kernel, dQ summed with
-   * floating-point atomics (not deterministic); stash: the dK/dV kernel
-   * writes the rounded dS it computes, and a dQ kernel reads it back instead
-   * of recomputing S and dP (deterministic; heads * n_ctx^2 * 2 bytes of
-   * workspace); merged: the split's dK/dV and dQ kernels in one grid (dQ
-   * workgroups fill the dK/dV tail; deterministic, bit-identical to the
-   * split, no workspace).  The reference's split (attn_bwd_dq +
-   * attn_bwd_dkdv) stays available in every library. */
-  enum class Bwd { Split, Atomic, Stash, Merged } bwd = Bwd::Split;
+  /* bwd=atomic: the library also offers attn_bwd_fused, a backward in one
+   * call (one dK/dV/dQ kernel, dQ summed with floating-point atomics, not
+   * deterministic).  The reference's split (attn_bwd_dq + attn_bwd_dkdv)
+   * stays available in every library. */
+  enum class Bwd { Split, Atomic } bwd = Bwd::Split;
 
   std::string text() const {
     return format("builtin element=%s head_dim=%d causal=%d%s", element_name(element), head_dim,
                   causal ? 1 : 0,
-                  bwd == Bwd::Atomic   ? " bwd=atomic"
-                  : bwd == Bwd::Stash  ? " bwd=stash"
-                  : bwd == Bwd::Merged ? " bwd=merged"
-                                       : "");
+                  bwd == Bwd::Atomic ? " bwd=atomic" : "");
   }
 };
 
@@ -247,11 +239,17 @@ struct Library : Object {
   /* explicit parameters of each kernel, from the code object's metadata
    * (empty when the image carries none this library can read) */
   std::map<std::string, std::vector<tm_codeobject::ArgSlot>> signatures;
-  /* bwd=atomic: the fp32 dQ accumulator of attn_bwd_fused, grown on demand
-   * (launches of one library are ordered on its stream, so one suffices) */
+  /* work memory of planned dispatch sequences (GEMM K-range partials, the
+   * generic attention kernels' range partials, the fp32 dQ accumulator of
+   * attn_bwd_fused): see plan_workspace */
   mutable std::mutex workspace_lock;
   mutable void *workspace = nullptr;
   mutable size_t workspace_bytes = 0;
+  /* held by a launch from planning (which may hand out, grow or shrink the
+   * workspace) until its whole dispatch sequence is queued: two threads
+   * launching on one library then neither free a workspace the other's
+   * planned dispatches still bind nor interleave their sequences */
+  std::mutex launch_lock;
   ~Library() override {
     if (!module && !workspace) return;
     /* a dispatch of one of its kernels may still be queued (tm_launch_async):
@@ -387,10 +385,7 @@ BuiltinSpec parse_spec(const char *text) {
     } else if (key == "bwd") {
       if (value == "split") spec.bwd = BuiltinSpec::Bwd::Split;
       else if (value == "atomic") spec.bwd = BuiltinSpec::Bwd::Atomic;
-      else if (value == "stash") spec.bwd = BuiltinSpec::Bwd::Stash;
-      else if (value == "merged") spec.bwd = BuiltinSpec::Bwd::Merged;
-      else throw TmError("built-in library spec: bwd must be split, atomic, stash or merged, got '" + value +
-                         "'");
+      else throw TmError("built-in library spec: bwd must be split or atomic, got '" + value + "'");
     } else {
       throw TmError("built-in library spec: unknown key '" + key + "'");
     }
@@ -763,14 +758,23 @@ struct Scratch {
   size_t bytes = 0;
 };
 
+/* A workspace above this size is given back when a later sequence needs less
+ * than a quarter of it, so one large request does not pin its memory for the
+ * library's lifetime. */
+constexpr size_t kWorkspaceKeepBytes = (size_t)256 << 20;
+
 /* `need` bytes of device work memory for one planned dispatch sequence: the
  * static scratch under tm_launch_noalloc (nullptr when it is too small), else
- * the library's workspace, grown on demand.  Dispatches of one library run in
- * order on its stream, so consecutive sequences may share the workspace. */
+ * the library's workspace, grown on demand and shrunk after a large request.
+ * Dispatches of one library run in order on its stream, so consecutive
+ * sequences may share the workspace; the caller holds the library's
+ * launch_lock until its sequence is queued, so no other launch replaces the
+ * workspace in between. */
 void *plan_workspace(const Library &lib, size_t need, const Scratch *scratch) {
   if (scratch) return need <= scratch->bytes ? scratch->ptr : nullptr;
   std::lock_guard<std::mutex> guard(lib.workspace_lock);
-  if (lib.workspace_bytes < need) {
+  const bool shrink = lib.workspace_bytes > kWorkspaceKeepBytes && need < lib.workspace_bytes / 4;
+  if (lib.workspace_bytes < need || shrink) {
     /* the old workspace may still be bound to a queued dispatch */
     if (lib.workspace) {
       finish(require_device().stream);
@@ -829,90 +833,6 @@ bool plan_gemm_split(Plan &plan, TmGemmArgs &p, const BuiltinSpec &spec, const L
   return true;
 }
 
-/* attn_bwd_fused under bwd=stash as two dispatches: the dK/dV kernel, which
- * also writes dS^T into `stash`, then the dQ kernel that reads it.  Every
- * stash element the dQ kernel reads for a stored query is written first (the
- * causal dK/dV walk starts at its key block's first key, the dQ walk stops at
- * its query block's last key; keys up to the next multiple of 128 are
- * written), so nothing needs clearing; unwritten elements reach only the
- * columns of queries past n_ctx, which are not stored. */
-void plan_stash_backward(Plan &plan, const BuiltinSpec &spec, const TmAttnDkdvArgs &kv, void *dq,
-                         void *stash, int32_t stash_keys, int32_t stash_blocks) {
-  const char *el = element_name(spec.element);
-  TmAttnFusedArgs f{};
-  f.kv = kv;
-  f.dq = dq;
-  f.stash = stash;
-  f.stash_keys = stash_keys;
-  f.stash_blocks = stash_blocks;
-  Plan kv_pass, dq_pass;
-  kv_pass.variant = format("tm_attn_dkdv_stash_%s_d%d%s", el, spec.head_dim,
-                           spec.causal ? "_causal" : "");
-  kv_pass.grid[0] = (unsigned)(cdiv(kv.n_ctx, 128) * kv.heads);
-  kv_pass.block = 256;
-  set_kernarg(kv_pass, f);
-  dq_pass.variant = format("tm_attn_dq_stash_%s_d%d%s", el, spec.head_dim,
-                           spec.causal ? "_causal" : "");
-  dq_pass.grid[0] = (unsigned)(cdiv(kv.n_ctx, 256) * kv.heads);
-  dq_pass.block = 512;
-  set_kernarg(dq_pass, f);
-  for (Plan *part : {&kv_pass, &dq_pass}) part->function = builtin_function(part->variant);
-  plan.variant = kv_pass.variant;
-  plan.function = kv_pass.function;
-  plan.block = kv_pass.block;
-  plan.sequence = {kv_pass, dq_pass};
-}
-
-/* attn_bwd_fused under bwd=merged: at head_dim 128 one dispatch of
- * tm_attn_bwd_merged_* over the dK/dV grid followed by the dQ grid (both
- * cdiv(n_ctx, 128) * heads workgroups of 256 threads); at head_dim 64, whose
- * dK/dV kernel runs one wave per SIMD and dQ three, the two split kernels back
- * to back.  Either way dQ, dK and dV are the split's, bit for bit. */
-void plan_merged_backward(Plan &plan, const BuiltinSpec &spec, const TmAttnDkdvArgs &kv, void *dq) {
-  const char *el = element_name(spec.element);
-  const char *cn = spec.causal ? "_causal" : "";
-  const unsigned wgs = (unsigned)(cdiv(kv.n_ctx, 128) * kv.heads);
-  TmAttnDqArgs q{};
-  q.q = kv.q;
-  q.k = kv.k;
-  q.v = kv.v;
-  q.dout = kv.dout;
-  q.dq = dq;
-  q.lse = kv.lse;
-  q.delta = kv.delta;
-  q.sm_scale = kv.sm_scale;
-  q.stride_head = kv.stride_head;
-  q.stride_seq = kv.stride_seq;
-  q.stride_lse = kv.stride_lse;
-  q.n_ctx = kv.n_ctx;
-  q.head_dim = kv.head_dim;
-  q.heads = kv.heads;
-  if (spec.head_dim == 128) {
-    TmAttnFusedArgs f{};
-    f.kv = kv;
-    f.dq = dq;
-    plan.variant = format("tm_attn_bwd_merged_%s_d128%s", el, cn);
-    plan.grid[0] = 2 * wgs;
-    plan.block = 256;
-    set_kernarg(plan, f);
-    plan.function = builtin_function(plan.variant);
-    return;
-  }
-  Plan kv_pass, dq_pass;
-  kv_pass.variant = format("tm_attn_dkdv_fast_%s_d%d%s", el, spec.head_dim, cn);
-  kv_pass.grid[0] = wgs;
-  kv_pass.block = 256;
-  set_kernarg(kv_pass, kv);
-  dq_pass.variant = format("tm_attn_dq_fast_%s_d%d%s", el, spec.head_dim, cn);
-  dq_pass.grid[0] = wgs;
-  dq_pass.block = 256;
-  set_kernarg(dq_pass, q);
-  for (Plan *part : {&kv_pass, &dq_pass}) part->function = builtin_function(part->variant);
-  plan.variant = kv_pass.variant;
-  plan.function = kv_pass.function;
-  plan.block = kv_pass.block;
-  plan.sequence = {kv_pass, dq_pass};
-}
 
 /* Ranges to split a generic attention kernel's walk into when its grid of
  * `wgs` 64-row workgroups cannot fill the chip twice: enough to (at most 16,
@@ -1283,35 +1203,16 @@ Plan plan_builtin(Kernel &k, const Library &lib, const std::vector<Arg> &args, i
       kv.sm_scale = sm_scale;
       kv.head_dim = spec.head_dim;
       kv.heads = (int32_t)heads;
-      if (spec.bwd == BuiltinSpec::Bwd::Merged) {
-        plan_merged_backward(plan, spec, kv, args[4].buffer->ptr);
-        return plan;
-      }
-      const bool stash = spec.bwd == BuiltinSpec::Bwd::Stash;
-      /* atomic: the fp32 dQ accumulator; stash: dS^T per head as [query
-       * blocks of 32, rounded up to whole 256-query blocks][keys rounded up
-       * to 128][32] */
+      /* the fp32 dQ accumulator */
       const int64_t count = heads * kv.n_ctx * (int64_t)spec.head_dim;
-      const int64_t stash_keys = cdiv(kv.n_ctx, 128) * 128;
-      const int64_t stash_blocks = cdiv(kv.n_ctx, 256) * 8;
-      const int64_t stash_head = stash_blocks * stash_keys * 32 * 2;
-      if (stash && stash_head > INT32_MAX)
-        throw TmError(format("%s with bwd=stash keeps n_ctx^2 elements of dS per head and takes "
-                             "n_ctx up to 32640; got %d",
-                             nm, kv.n_ctx));
-      const size_t need = stash ? (size_t)(heads * stash_head) : (size_t)count * sizeof(float);
+      const size_t need = (size_t)count * sizeof(float);
       void *work = plan_workspace(lib, need, scratch);
       if (!work)
-        throw TmError(format("%s through tm_launch_noalloc needs a %zu-byte %s but the static "
-                             "scratch holds %zu bytes; launch it with tm_launch",
-                             nm, need,
-                             stash ? "dS stash (heads * n_ctx * n_ctx rounded up to 128 * 2)"
-                                   : "dQ accumulator (heads * n_ctx * head_dim * 4)",
-                             scratch->bytes));
-      if (stash)
-        plan_stash_backward(plan, spec, kv, args[4].buffer->ptr, work, (int32_t)stash_keys,
-                            (int32_t)stash_blocks);
-      else plan_fused_backward(plan, spec, kv, args[4].buffer->ptr, (float *)work, count);
+        throw TmError(format("%s through tm_launch_noalloc needs a %zu-byte dQ accumulator "
+                             "(heads * n_ctx * head_dim * 4) but the static scratch holds %zu "
+                             "bytes; launch it with tm_launch",
+                             nm, need, scratch->bytes));
+      plan_fused_backward(plan, spec, kv, args[4].buffer->ptr, (float *)work, count);
       return plan;
     }
     case Builtin::Probe: {
@@ -1476,11 +1377,14 @@ void enqueue(const Plan &plan, hipStream_t stream) {
  * except the device lookup the built-in planner needs. */
 Plan prepare(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_t threads,
              const int32_t *kinds, const int64_t *values, int32_t argc,
-             std::shared_ptr<Kernel> &k_out,
+             std::shared_ptr<Kernel> &k_out, std::unique_lock<std::mutex> &launch_guard,
              std::vector<std::shared_ptr<Buffer>> *mirrored = nullptr,
              const Scratch *scratch = nullptr) {
   auto k = handles().lookup<Kernel>(kernel, Kind::Kernel, "kernel");
   k_out = k;
+  /* from here until the caller has queued the plan, no other launch on this
+   * library plans or queues */
+  launch_guard = std::unique_lock<std::mutex>(k->library->launch_lock);
   std::vector<Arg> args = decode_args(kinds, values, argc);
   if (mirrored)
     for (const Arg &a : args)
@@ -1591,7 +1495,9 @@ int64_t launch_common(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_
                       int32_t repeats, float *elapsed_ms, const Scratch *scratch = nullptr) {
   std::shared_ptr<Kernel> k;
   std::vector<std::shared_ptr<Buffer>> mirrored;
-  Plan plan = prepare(kernel, gx, gy, gz, threads, kinds, values, argc, k, &mirrored, scratch);
+  std::unique_lock<std::mutex> launch_guard;
+  Plan plan = prepare(kernel, gx, gy, gz, threads, kinds, values, argc, k, launch_guard, &mirrored,
+                      scratch);
   Device &dev = require_device();
   /* buffers with a host mirror: mirror -> HBM before, HBM -> mirror after */
   for (const auto &b : mirrored) {
@@ -1610,6 +1516,7 @@ int64_t launch_common(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_
   };
   if (repeats <= 0) {
     enqueue(plan, dev.stream);
+    launch_guard.unlock();
     if (wait) finish(dev.stream);
     refresh_mirrors();
     return 0;
@@ -1624,6 +1531,7 @@ int64_t launch_common(int64_t kernel, int64_t gx, int64_t gy, int64_t gz, int64_
   hip_check(hipEventRecord(start, dev.stream), "hipEventRecord");
   for (int i = 0; i < repeats; ++i) enqueue(plan, dev.stream);
   hip_check(hipEventRecord(stop, dev.stream), "hipEventRecord");
+  launch_guard.unlock();
   finish(dev.stream);
   float ms = 0.f;
   hip_check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
@@ -1784,9 +1692,7 @@ int64_t tm_load_kernel(int64_t library, const char *name) {
                            builtin_names().c_str()));
     if (info->id == Builtin::AttnFused && lib->spec.bwd == BuiltinSpec::Bwd::Split)
       throw TmError("kernel 'attn_bwd_fused' is offered only by built-in libraries whose spec "
-                    "has bwd=atomic (dQ summed with floating-point atomics, not deterministic) "
-                    "or bwd=stash (dS kept in a workspace for the dQ pass) or bwd=merged (the "
-                    "split's dK/dV and dQ kernels in one grid)");
+                    "has bwd=atomic (dQ summed with floating-point atomics, not deterministic)");
     k->builtin = info->id;
     /* load the kernel images now, so that launches (tm_launch_noalloc among
      * them) load no code; a failure here resurfaces at the first launch */
@@ -1877,6 +1783,23 @@ void *tm_buffer_contents(int64_t buffer) {
   }
   return buf->host;
   TM_GUARD_END(nullptr)
+}
+
+int32_t tm_buffer_unmap(int64_t buffer) {
+  TM_GUARD_BEGIN
+  auto buf = handles().lookup<Buffer>(buffer, Kind::Buffer, "buffer");
+  /* launches that bound the buffer have refreshed the mirror when they
+   * returned; host writes since then are copied down before it goes */
+  finish(require_device().stream);
+  std::lock_guard<std::mutex> guard(buf->host_lock);
+  if (buf->host) {
+    hip_check(hipMemcpy(buf->ptr, buf->host, (size_t)buf->length, hipMemcpyHostToDevice),
+              "hipMemcpy (host mirror to HBM)");
+    hip_check(hipHostFree(buf->host), "hipHostFree");
+    buf->host = nullptr;
+  }
+  return 0;
+  TM_GUARD_END(-1)
 }
 
 int64_t tm_buffer_length(int64_t buffer) {

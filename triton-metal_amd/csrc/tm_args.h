@@ -104,19 +104,14 @@ struct TmAttnDkdvArgs {
   int32_t splits;
 };
 
-/* attn_bwd_fused (built-in libraries with bwd=atomic, bwd=stash or bwd=merged; no
- * reference kernel — the single-pass variant the reference names at
+/* attn_bwd_fused (built-in libraries with bwd=atomic; no reference kernel —
+ * the single-pass variant the reference names at
  * AttentionBackwardKernel.swift:27-41 and docs/COMPARISON.md:151-154): the
- * dK/dV kernel's arguments plus, for bwd=atomic, dQ's fp32 accumulator
- * ([heads][n_ctx][head_dim] dense, zeroed before the launch), or, for
- * bwd=stash, dQ and the dS^T stash the dK/dV pass writes for the dQ pass, or,
- * for bwd=merged, dQ. */
+ * dK/dV kernel's arguments plus dQ's fp32 accumulator ([heads][n_ctx][head_dim]
+ * dense, zeroed before the launch). */
 struct TmAttnFusedArgs {
   TmAttnDkdvArgs kv;
-  float *dq_acc;   /* bwd=atomic */
-  void *dq;        /* bwd=stash: dQ, and the dS^T stash, per head */
-  void *stash;     /* [stash_blocks query blocks of 32][stash_keys][32] */
-  int32_t stash_keys, stash_blocks;
+  float *dq_acc;
 };
 
 /* The passes around attn_bwd_fused: clear dq_acc (count floats), then write

@@ -85,6 +85,7 @@ _SIGNATURES = {
         _i32,
         [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_i32), ctypes.POINTER(_i64), _i32],
     ),
+    "tm_buffer_unmap": (_i32, [_i64]),
 }
 
 #: The exports the reference's C ABI has (reference _core.py:70-100).
@@ -194,8 +195,16 @@ def alloc_buffer(nbytes: int) -> int:
 
 
 def buffer_contents(handle: int) -> int:
-    """Device address of the buffer (what a kernel dereferences)."""
+    """Host address of the buffer's contents: its pinned host mirror, made on
+    the first call.  While the mirror exists every launch that binds the
+    buffer copies it to HBM and back and waits; buffer_unmap drops it."""
     return _check(_lib.tm_buffer_contents(handle), None)
+
+
+def buffer_unmap(handle: int) -> None:
+    """Drop the host mirror (host writes through it reach HBM first); the
+    address buffer_contents gave is invalid afterwards."""
+    _check(_lib.tm_buffer_unmap(handle), -1)
 
 
 def buffer_length(handle: int) -> int:

@@ -6,7 +6,8 @@ same constructor arguments, dtype names, `data_ptr`, `copy_from`/`copy_to`,
 memory.  `data_ptr()` is `tm_buffer_contents`: a host address that behaves like
 the reference's unified memory (the library keeps a pinned host mirror of a
 buffer once it has been asked for one, and copies it around each launch that
-binds the buffer), so code that reads or writes through it works unchanged.
+binds the buffer, and waits), so code that reads or writes through it works
+unchanged; `unmap()` drops the mirror.
 The copies `copy_from`/`copy_to`/`numpy`/`write` are `tm_buffer_write`/
 `tm_buffer_read` and never create a mirror.
 
@@ -77,8 +78,19 @@ class DeviceBuffer:
         self.tm_handle = _core.alloc_buffer(self.nbytes)
 
     def data_ptr(self):
-        """Host address of the contents (the buffer's host mirror)."""
+        """Host address of the contents (the buffer's host mirror).
+
+        The first call makes a pinned host copy of the whole buffer.  From
+        then on every launch that binds the buffer copies it host -> HBM
+        before the dispatch and back after it, and waits for it (launch_async
+        included): a caller that only wants a pointer pays two full-buffer
+        copies and a synchronisation per launch.  `unmap()` ends that."""
         return _core.buffer_contents(self.tm_handle)
+
+    def unmap(self):
+        """Drop the host mirror made by `data_ptr()` (writes through it reach
+        HBM first); the address it returned is invalid afterwards."""
+        _core.buffer_unmap(self.tm_handle)
 
     def __len__(self):
         return self.shape[0] if self.shape else 0

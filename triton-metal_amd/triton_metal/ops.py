@@ -31,12 +31,9 @@ def cdiv(a, b):
 
 
 class BuiltinLibrary:
-    """One built-in library spec and its kernels, loaded once.  bwd="atomic",
-    "stash" or "merged" adds attn_bwd_fused, the backward in one call: atomic
-    sums dQ with fp32 atomics (not deterministic); stash keeps the dS the dK/dV
-    pass computes for a dQ pass (deterministic, n_ctx^2 workspace per head);
-    merged runs the split's dK/dV and dQ kernels in one grid (bit-identical to
-    the split)."""
+    """One built-in library spec and its kernels, loaded once.  bwd="atomic"
+    adds attn_bwd_fused, the backward in one call that sums dQ with fp32
+    atomics (not deterministic)."""
 
     NAMES = ("matmul_kernel", "attn_fwd", "attn_bwd_preprocess", "attn_bwd_dq", "attn_bwd_dkdv",
              "sae_encode_kernel")
@@ -44,8 +41,8 @@ class BuiltinLibrary:
     def __init__(self, element="f32", head_dim=64, causal=False, bwd="split"):
         if element not in _ELEMENTS:
             raise ValueError(f"element must be one of {sorted(_ELEMENTS)}")
-        if bwd not in ("split", "atomic", "stash", "merged"):
-            raise ValueError("bwd must be 'split', 'atomic', 'stash' or 'merged'")
+        if bwd not in ("split", "atomic"):
+            raise ValueError("bwd must be 'split' or 'atomic'")
         self.element = element
         self.dtype = _ELEMENTS[element]
         self.head_dim = head_dim
@@ -208,7 +205,7 @@ class AttentionLayer:
 
     `heads` is batch*heads: the reference's layout [B*H, S, D] with
     stride_head = S*D and stride_seq = D (AttentionKernel.swift:25-28).
-    bwd="atomic", "stash" or "merged" runs the backward as preprocess + attn_bwd_fused
+    bwd="atomic" runs the backward as preprocess + attn_bwd_fused
     instead of preprocess + dq + dkdv.
     """
 
