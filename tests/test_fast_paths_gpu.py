@@ -225,7 +225,8 @@ def _tile_suffix(m, n, cus=256, k=None):
 def test_fast_gemm_shapes_and_strides(element, m, n, k, lda, ldb, ldc, tile, device):
     c, want, variant = _gemm(m, n, k, element, lda, ldb, ldc)
     assert tile == _tile_suffix(m, n, k=k)
-    assert variant == f"tm_gemm_fast{tile}_{element}"
+    # whole row-major 256 x 256 tiles run the 4-wave kernel
+    assert variant == (f"tm_gemm_w4_{element}" if tile == "" else f"tm_gemm_fast{tile}_{element}")
     assert T.hybrid_error(c[:, :n], want) <= 2e-2
     if ldc:
         assert np.all(c[:, n:] == -7.0)
@@ -466,7 +467,7 @@ def test_gemm_layout_sweep(m, n, k, layout, pk, pn, pm, element, device):
     (512, 256, 128, None, None, "fast_t64_k4"),
     (2048, 2048, 64, None, None, "fast_t128"),
     (2000, 2100, 72, None, 2104, "ragged_t128"),
-    (4096, 4096, 64, None, None, "fast"),
+    (4096, 4096, 64, None, None, "w4"),
 ])
 def test_gemm_kernel_choice(m, n, k, lda, ldb, variant, device):
     c, want, got = _gemm(m, n, k, "bf16", lda, ldb)
@@ -516,3 +517,24 @@ def test_head_span_at_the_buffer_resource_limit(seq, expect, device):
     o_want, _, lse_want = R.attention_forward(q, k, v, 1 / math.sqrt(dim), False)
     assert T.max_abs_error(o, o_want) <= 2e-2
     assert T.max_abs_error(lse_got, lse_want) <= 2e-3
+
+
+@pytest.mark.parametrize("element", ["bf16", "f16"])
+@pytest.mark.parametrize("m,n,k,lda,ldb,ldc", [
+    (4096, 4096, 64, None, None, None),        # one K step: no copy of a next step
+    (4096, 4096, 128, None, None, None),       # two steps: each stage buffer once
+    (4096, 4608, 192, None, None, None),       # odd step count; 16 x 18 tiles
+    (5120, 4096, 1024, 1032, 4104, 4100),      # padded, poisoned leading dimensions
+    (8192, 4096, 320, None, None, None),
+])
+def test_four_wave_gemm(element, m, n, k, lda, ldb, ldc, device):
+    """The 4-wave 256 x 256-tile kernel (whole row-major tiles, K a multiple of
+    64): every element against fp64, padding columns of A and B poisoned
+    (inf, NaN) so a read past K or N reaches an output, C's padding and extra
+    rows untouched."""
+    c, want, variant = _gemm(m, n, k, element, lda, ldb, ldc, seed=k, poison=lda is not None,
+                             extra_rows=8)
+    assert variant == f"tm_gemm_w4_{element}"
+    assert np.all(np.isfinite(c[:m, :n]))
+    assert T.hybrid_error(c[:m, :n], want) <= 2e-2
+    assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)

@@ -77,7 +77,11 @@ def test_every_barrier_waits_for_the_waves_own_lds_copies():
             if not any(K.is_lds_dma(mn, ops) for _, mn, ops, _ in insns):
                 continue
             checked += 1
-            bad = K.barriers_with_copy_in_flight(insns, 0)
+            # the 4-wave GEMM issues half of its second tile's copies before
+            # its first barrier (they land by the second, before any wave
+            # reads that tile): one barrier in flight
+            depth = 1 if name.startswith(("tm_gemm_w4_", "tm_sae_w4_")) else 0
+            bad = K.barriers_with_copy_in_flight(insns, depth)
             assert not bad, f"{name}: s_barrier at {[hex(a) for a in bad]} with an LDS copy in flight"
     assert checked >= 40  # the specialised attention and GEMM kernels
 

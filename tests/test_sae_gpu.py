@@ -116,7 +116,7 @@ def test_short_buffers_are_refused(device):
     (100, 300, 700, "generic"),      # rows not 16-byte aligned
     (100, 512, 1000, "ragged_t64"),  # M and N short of whole tiles
     (333, 136, 264, "ragged_t64"),   # ragged K
-    (4096, 256, 4096, "fast"),       # 256 tiles of 256 x 256: one per compute unit
+    (4096, 256, 4096, "w4"),         # 256 tiles of 256 x 256: one per compute unit (4-wave kernel)
     (4000, 264, 4104, "ragged"),
 ])
 def test_16bit_matches_the_oracle(device, element, rows, model, features, variant):

@@ -604,6 +604,17 @@ void validate_attn_common(const char *name, int64_t heads, int32_t stride_head,
   if (heads > 65535) throw TmError(format("%s: %lld heads exceeds 65535", name, (long long)heads));
 }
 
+/* TRITON_METAL_GEMM_W4=0 keeps whole 256 x 256-tile row-major GEMMs on the
+ * 8-wave kernel instead of the 4-wave one (A/B comparisons). */
+bool gemm_w4_enabled() {
+  static const bool enabled = [] {
+    const char *v = getenv("TRITON_METAL_GEMM_W4");
+    return !(v && strcmp(v, "0") == 0);
+  }();
+  return enabled;
+}
+
+
 /* 0 turns the bf16/f16 GEMM's K split across workgroups off (measurement builds) */
 #ifndef TM_GEMM_SPLITK
 #define TM_GEMM_SPLITK 1
@@ -701,6 +712,14 @@ void choose_gemm(Plan &plan, const TmGemmArgs &p, const BuiltinSpec &spec, const
                           kg == 4 ? "_k4" : kg == 2 ? "_k2" : "", el);
     plan.grid[0] = (unsigned)tiles;
     plan.block = (unsigned)(2 * tile * kg);
+    /* whole row-major 256 x 256 tiles: the 4-wave kernel (gemm_w4.hip), whose
+     * copies address a step's 256 rows of A and 64 rows of B through one
+     * 32-bit buffer range each */
+    if (gemm_w4_enabled() && nn && whole && big && (int64_t)p.sam * 512 <= INT32_MAX &&
+        (int64_t)p.sbk * 128 <= INT32_MAX) {
+      plan.variant = format("tm_%s_w4_%s", family, el);
+      plan.block = 256;
+    }
   } else {
     plan.variant = format("tm_%s_generic_%s", family, el);
     plan.grid[0] = (unsigned)cdiv(p.m, 64);
