@@ -89,7 +89,7 @@ COPY_BYTES = 1 << 30
 def profile_pass(core, ops):
     """One copy of COPY_BYTES (reads and writes that many bytes of HBM), then one
     dispatch each of attn_fwd, attn_bwd_preprocess, attn_bwd_dq, attn_bwd_dkdv at
-    config 5, the bwd=atomic backward (attn_bwd_fused: accumulator clear, fused
+    config 5, attn_fwd at config 4, the bwd=atomic backward (attn_bwd_fused: accumulator clear, fused
     kernel, dQ conversion) at config 5, matmul_kernel at config 3 and
     sae_encode_kernel at 8192 x 2048 x 16384."""
     from triton_metal.buffer import DeviceBuffer
@@ -108,6 +108,12 @@ def profile_pass(core, ops):
     layer.run_forward()
     layer.run_backward()
     layer.free()
+    # config 4: the D = 64 forward
+    c4 = ops.AttentionLayer(8 * 16, 1024, 64, "bf16", False)
+    for i, name in enumerate(("q", "k", "v")):
+        c4.buffers[name].write(normal_bf16((8 * 16, 1024, 64), 100 + i))
+    c4.run_forward()
+    c4.free()
     for mode in ("atomic",):
         fused = ops.AttentionLayer(B * H, S, D, "bf16", True, bwd=mode)
         for i, name in enumerate(("q", "k", "v", "do")):
