@@ -342,7 +342,7 @@ def _gemm_nt(m, n, k, element, lda=None, ldbt=None, ldc=None, seed=0):
 @pytest.mark.parametrize("element", ["bf16", "f16"])
 @pytest.mark.parametrize("m,n,k,lda,ldbt,ldc,kind", [
     (256, 256, 64, None, None, None, "fast"),
-    (4096, 4096, 128, None, None, None, "fast"),
+    (4096, 4096, 128, None, None, None, "w4"),
     (129, 257, 65, 72, 72, 260, "ragged"),
     (300, 1000, 136, None, None, None, "ragged"),
     (4000, 4100, 200, 200, 208, 4100, "ragged"),
@@ -386,7 +386,7 @@ def _gemm_tn(m, n, k, element, ldat=None, ldb=None, ldc=None, seed=0):
 @pytest.mark.parametrize("element", ["bf16", "f16"])
 @pytest.mark.parametrize("m,n,k,ldat,ldb,ldc,kind", [
     (256, 256, 64, None, None, None, "fast"),
-    (4096, 4096, 128, None, None, None, "fast"),
+    (4096, 4096, 128, None, None, None, "w4"),
     (129, 257, 65, 136, 264, 260, "ragged"),
     (1000, 300, 136, None, 304, None, "ragged"),
     (4100, 4000, 200, 4104, 4000, 4000, "ragged"),
@@ -535,6 +535,30 @@ def test_four_wave_gemm(element, m, n, k, lda, ldb, ldc, device):
     c, want, variant = _gemm(m, n, k, element, lda, ldb, ldc, seed=k, poison=lda is not None,
                              extra_rows=8)
     assert variant == f"tm_gemm_w4_{element}"
+    assert np.all(np.isfinite(c[:m, :n]))
+    assert T.hybrid_error(c[:m, :n], want) <= 2e-2
+    assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)
+
+
+@pytest.mark.parametrize("element", ["bf16", "f16"])
+@pytest.mark.parametrize("layout,m,n,k,lda,ldb,ldc", [
+    ("nt", 4096, 4096, 64, None, None, None),    # one K step
+    ("nt", 4096, 4608, 192, None, None, None),   # odd step count, 16 x 18 tiles
+    ("nt", 5120, 4096, 1024, 1032, 1040, 4100),  # padded, poisoned leading dimensions
+    ("tn", 4096, 4096, 64, None, None, None),
+    ("tn", 4608, 4096, 192, None, None, None),
+    ("tn", 4096, 5120, 1024, 4104, 5128, 5124),
+])
+def test_four_wave_gemm_transposed(element, layout, m, n, k, lda, ldb, ldc, device):
+    """The 4-wave kernel with B stored transposed (both operands K-contiguous,
+    read by ds_read_b128) or A stored transposed (both read transposed):
+    every element against fp64, operand padding poisoned, C's padding and
+    extra rows untouched."""
+    if layout == "nt":
+        c, want, variant = _gemm_nt(m, n, k, element, lda, ldb, ldc, seed=k)
+    else:
+        c, want, variant = _gemm_tn(m, n, k, element, lda, ldb, ldc, seed=k)
+    assert variant == f"tm_gemm_w4_{layout}_{element}"
     assert np.all(np.isfinite(c[:m, :n]))
     assert T.hybrid_error(c[:m, :n], want) <= 2e-2
     assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)

@@ -1,6 +1,8 @@
 /*
  * gfx950 GEMM for large whole-tile 16-bit problems: C = A @ B, A [M, K] and
- * B [K, N] row-major, M and N multiples of 256, K a multiple of 64; f32
+ * B [K, N] row-major, or one of them stored transposed (B as [N, K]: the
+ * x @ W^T layout; A as [K, M]: the dY^T X layout), M and N multiples of 256,
+ * K a multiple of 64; f32
  * accumulation, output rounded to the element type (the reference's
  * matmul_kernel semantics, Sources/TritonMetalBench/GEMMKernel.swift:28-174),
  * optionally with the SAE encoder's bias + ReLU epilogue
@@ -28,17 +30,21 @@
  * Measured at 8192^3 on one MI355X (alternating runs, TFLOP/s): this kernel
  * 1311-1342 against 1291-1341 for gemm_fast.hip's 8-wave kernel, the SAE
  * encoder shape (8192 x 2048 -> 16384) 1166 against 1080, and short K
- * (4096^2 x 64 / 128) 11.6 / 12.7 us against 14.1 / 15.3.  Without its copies
+ * (4096^2 x 64 / 128) 11.6 / 12.7 us against 14.1 / 15.3; B transposed
+ * 1315-1321 against 1289-1298, A transposed 1297-1304 against 1218-1222.
+ * Without its copies
  * (timing only) it runs 1690 (constant operands): one wave per SIMD cannot
  * hide the issue of the copy instructions behind another wave's MFMAs.
  *
  * Operands (lane l, h = l / 32): the MFMA's first operand is a B fragment
- * (C column n0 + (l % 32), k = 8h .. 8h + 7), two ds_read_b64_tr_b16 of the
- * row-major B tile; the second an A fragment (C row m0 + (l % 32), the same
- * k), one ds_read_b128.  The product is then C^T: a lane holds 4 consecutive
- * columns of one row per group of 4 accumulator floats, stored as one 8-byte
- * write.  Tiles keep gemm_fast.hip's row-major layouts (A rows of 128 bytes,
- * B rows of 512 bytes) with XOR keys for this kernel's 32-row reads.
+ * (C column n0 + (l % 32), k = 8h .. 8h + 7), the second an A fragment (C row
+ * m0 + (l % 32), the same k).  A K-contiguous operand (A row-major, B
+ * transposed) keeps its stored rows in a [256][64] tile of 128-byte rows and
+ * gives a fragment by one ds_read_b128; the other kind a [64][256] tile of
+ * 512-byte rows and two ds_read_b64_tr_b16 (W4Operand).  The product is then
+ * C^T: a lane holds 4 consecutive columns of one row per group of 4
+ * accumulator floats.  Tiles keep gemm_fast.hip's layouts with XOR keys for
+ * this kernel's 32-row reads.
  */
 #include "common.h"
 
@@ -117,7 +123,66 @@ TM_DEV uint32_t w4_pack2(float lo, float hi) {
 
 #define W4_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-template <typename T, int EPI>
+/* One operand's tiles.  KC (K-contiguous: A row-major, or B stored
+ * transposed): [256 rows][64 k], 128-byte rows, keyed by w4_a_swz, copied 8
+ * rows per instruction and read by ds_read_b128.  MC (M- or N-contiguous: B
+ * row-major, or A stored transposed): [64 k][256 columns], 512-byte rows,
+ * keyed by w4_b_swz, copied 2 rows per instruction and read by two
+ * ds_read_b64_tr_b16.  Either way a fragment f (0..3) of substep s (k 16s ..
+ * 16s + 15) gives lane l the 8 values k = 16s + 8h .. + 7 (h = l / 32) of
+ * tile row or column half * 128 + 32 f + l % 32, the operand layout of
+ * v_mfma_f32_32x32x16. */
+template <typename T, bool KC>
+struct W4Operand {
+  const T *base;  /* the tile's origin at k = 0 */
+  int64_t ld;     /* elements between the tile's stored rows */
+  uint32_t bytes; /* a step's buffer range */
+  int voff[2];    /* copy lane offsets by instruction parity */
+  uint32_t rd[4]; /* read lane offsets: per substep (KC) or per fragment (MC) */
+  TM_DEV void init(const T *origin, int64_t stride, int lane, int half) {
+    base = origin;
+    ld = stride;
+    if constexpr (KC) {
+      bytes = (uint32_t)((int64_t)(W4_TILE - 1) * ld * 2 + W4_BK * 2);
+#pragma unroll
+      for (int par = 0; par < 2; ++par)
+        voff[par] = (lane >> 3) * (int)ld * 2 + (((lane & 7) ^ w4_a_swz(8 * par + (lane >> 3))) << 4);
+      const int row = half * 128 + (lane & 31), h = lane >> 5;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) rd[s] = (uint32_t)w4_a_off(row, 2 * s + h);
+    } else {
+      bytes = (uint32_t)((int64_t)(W4_BK - 1) * ld * 2 + W4_TILE * 2);
+#pragma unroll
+      for (int par = 0; par < 2; ++par)
+        voff[par] = (lane >> 5) * (int)ld * 2 +
+                    (((lane & 31) ^ w4_b_swz(2 * par + (lane >> 5))) << 4);
+      const int q = lane >> 4, i = lane & 15;
+      const int krow = 8 * (q >> 1) + (i >> 2);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const int col = half * 128 + 32 * f + 16 * (q & 1) + 4 * (i & 3);
+        rd[f] = (uint32_t)(w4_b_off(krow, col >> 3) + (((col >> 2) & 1) << 3));
+      }
+    }
+  }
+  TM_DEV u32x4 rsrc(int kb) const {
+    return w4_rsrc(KC ? base + kb * W4_BK : base + (int64_t)kb * W4_BK * ld, bytes);
+  }
+  /* copy instruction t (0..31) of a step's tile into `region` */
+  TM_DEV void copy(const u32x4 &rs, int t, uint32_t region) const {
+    w4_copy16(rs, voff[t & 1], t * (KC ? 8 : 2) * (int)ld * 2, region + t * 1024);
+  }
+  TM_DEV u32x4 read(uint32_t region, int s, int f) const {
+    if constexpr (KC) return w4_lds_read16(region + rd[s] + f * 32 * 128);
+    const uint32_t ad = region + rd[f] + s * 16 * 512;
+    return w4_lds_read_tr(ad, ad + 4 * 512);
+  }
+};
+
+/* AK: A row-major [M, K] (else stored transposed, element (m, k) at
+ * k * stride_ak + m); BK: B stored transposed, element (k, n) at
+ * n * stride_bn + k (else row-major [K, N]). */
+template <typename T, int EPI, bool AK, bool BK>
 TM_DEV void gemm_w4(const TmGemmArgs &p) {
   typedef typename W4Vec8<T>::type v8;
   __shared__ __align__(1024) char lds[2 * W4_STAGE];
@@ -137,64 +202,26 @@ TM_DEV void gemm_w4(const TmGemmArgs &p) {
   const int in_group = logical - group * per_group;
   const int m0 = (first_m + in_group % gm) * W4_TILE, n0 = (in_group / gm) * W4_TILE;
 
-  const int64_t lda = p.sam, ldb = p.sbk, ldc = p.scm;
-  const T *A = (const T *)p.a + (int64_t)m0 * lda;
-  const T *B = (const T *)p.b + n0;
+  const int64_t ldc = p.scm;
+  W4Operand<T, AK> opa;
+  W4Operand<T, BK> opb;
+  opa.init(AK ? (const T *)p.a + (int64_t)m0 * p.sam : (const T *)p.a + m0, AK ? p.sam : p.sak,
+           lane, wm);
+  opb.init(BK ? (const T *)p.b + (int64_t)n0 * p.sbn : (const T *)p.b + n0, BK ? p.sbn : p.sbk,
+           lane, wn);
 
-  /* copies: A tile = 32 instructions of 8 rows, B tile = 32 of 2 rows; wave w
-   * issues instructions 8w .. 8w + 7 of each.  A: lane row (l >> 3), chunk
-   * (l & 7) ^ key(row) (the key depends on the lane and the instruction's
-   * parity); the instruction's rows go in soffset.  B: lane row (l >> 5) of the pair, chunk (l & 31) ^
-   * key(row), the key depending on the instruction's rows too. */
-  /* the A key of row 8t + (l >> 3) depends on t's parity */
-  int a_voff[2];
-#pragma unroll
-  for (int par = 0; par < 2; ++par)
-    a_voff[par] = (lane >> 3) * (int)lda * 2 + (((lane & 7) ^ w4_a_swz(8 * par + (lane >> 3))) << 4);
-  int b_voff[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = 2 * (wave * 8 + i) + (lane >> 5);
-    b_voff[i] = (lane >> 5) * (int)ldb * 2 + (((lane & 31) ^ w4_b_swz(row)) << 4);
-  }
-  /* buffer ranges: a step's A rows (256 x lda) and B rows (64 x ldb) */
-  const uint32_t a_bytes = (uint32_t)((int64_t)(W4_TILE - 1) * lda * 2 + W4_BK * 2);
-  const uint32_t b_bytes = (uint32_t)((int64_t)(W4_BK - 1) * ldb * 2 + W4_TILE * 2);
-  auto copy = [&](uint32_t stage, int kb, int i, const u32x4 &ra, const u32x4 &rb) {
-    /* instruction i of 16: A (i < 8) or B */
+  /* copies: each tile is 32 instructions of 1 KB; wave w issues instructions
+   * 8w .. 8w + 7 of each: copy i of 16 is A's (i < 8) or B's */
+  auto copy = [&](uint32_t stage, int i, const u32x4 &ra, const u32x4 &rb) {
     const int t = wave * 8 + (i & 7);
-    if (i < 8) w4_copy16(ra, a_voff[t & 1], t * 8 * (int)lda * 2, stage + t * 1024);
-    else w4_copy16(rb, b_voff[i & 7], t * 2 * (int)ldb * 2, stage + W4_A_BYTES + t * 1024);
-    (void)kb;
+    if (i < 8) opa.copy(ra, t, stage);
+    else opb.copy(rb, t, stage + W4_A_BYTES);
   };
-  auto rsrc_a = [&](int kb) { return w4_rsrc(A + kb * W4_BK, a_bytes); };
-  auto rsrc_b = [&](int kb) { return w4_rsrc(B + (int64_t)kb * W4_BK * ldb, b_bytes); };
-
-  /* operand offsets: A fragment i (rows wm*128 + 32i + l%32) at substep s
-   * (chunk 2s + h): a_lane[s] + 32 i * 128; B fragment j (columns
-   * wn*128 + 32j + 16 (q & 1) + lane-in-group, q = l / 16) at substep s (rows
-   * 16s + 8 (q >> 1) + (i >> 2), and +4): b_lane[j] + 16 s * 512 (+ 4 * 512) */
-  uint32_t a_lane[4], b_lane[4];
-  {
-    const int row = wm * 128 + (lane & 31), h = lane >> 5;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) a_lane[s] = (uint32_t)w4_a_off(row, 2 * s + h);
-    const int q = lane >> 4, i = lane & 15;
-    const int brow = 8 * (q >> 1) + (i >> 2);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = wn * 128 + 32 * j + 16 * (q & 1) + 4 * (i & 3);
-      b_lane[j] = (uint32_t)(W4_A_BYTES + w4_b_off(brow, n >> 3) + (((n >> 2) & 1) << 3));
-    }
-  }
   auto read_ops = [&](uint32_t stage, int s, u32x4 (&af)[4], u32x4 (&bf)[4]) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t ad = stage + b_lane[j] + s * 16 * 512;
-      bf[j] = w4_lds_read_tr(ad, ad + 4 * 512);
-    }
+    for (int f = 0; f < 4; ++f) bf[f] = opb.read(stage + W4_A_BYTES, s, f);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) af[i] = w4_lds_read16(stage + a_lane[s] + i * 32 * 128);
+    for (int f = 0; f < 4; ++f) af[f] = opa.read(stage, s, f);
   };
 
   f32x16 acc[4][4];
@@ -229,7 +256,7 @@ TM_DEV void gemm_w4(const TmGemmArgs &p) {
    * MFMAs of the window, 1342; every three, 1286; every four, 1190).
    * Copies 0-7 of step 1 (window MFMAs 0-15) go out in the prologue. */
   constexpr int SPREAD = 2, PRE1 = 16 / SPREAD;
-  auto copy_step = [&](uint32_t stage, int kb, int x) { copy(stage, kb, x, rsrc_a(kb), rsrc_b(kb)); };
+  auto copy_step = [&](uint32_t stage, int kb, int x) { copy(stage, x, opa.rsrc(kb), opb.rsrc(kb)); };
 #pragma unroll
   for (int x = 0; x < 16; ++x) copy_step(st0, 0, x);
   if (ksteps > 1) {
@@ -252,13 +279,13 @@ TM_DEV void gemm_w4(const TmGemmArgs &p) {
     constexpr bool NEXT2 = decltype(next2_tag)::value;
     const uint32_t cur = st0 + (uint32_t)((kb & 1) * W4_STAGE);
     const uint32_t nxt = st0 + (uint32_t)(((kb + 1) & 1) * W4_STAGE);
-    const u32x4 ra = rsrc_a(kb + 1), rb = rsrc_b(kb + 1);
+    const u32x4 ra = opa.rsrc(kb + 1), rb = opb.rsrc(kb + 1);
     /* step kb + 1's copies at window MFMAs 16-63 */
     auto copies_in = [&](int sub) {
       return [&, sub](int at) {
         if constexpr (NEXT) {
           const int pos = 16 + sub * 16 + at;
-          if (pos % SPREAD == 0 && pos / SPREAD < 16) copy(nxt, kb + 1, pos / SPREAD, ra, rb);
+          if (pos % SPREAD == 0 && pos / SPREAD < 16) copy(nxt, pos / SPREAD, ra, rb);
         }
       };
     };
@@ -279,9 +306,9 @@ TM_DEV void gemm_w4(const TmGemmArgs &p) {
     }
     if constexpr (NEXT2) {
       /* step kb + 2's copies at window MFMAs 0-15, into `cur` */
-      const u32x4 ra2 = rsrc_a(kb + 2), rb2 = rsrc_b(kb + 2);
+      const u32x4 ra2 = opa.rsrc(kb + 2), rb2 = opb.rsrc(kb + 2);
       mfmas(a1, b1, [&](int at) {
-        if (at % SPREAD == 0) copy(cur, kb + 2, at / SPREAD, ra2, rb2);
+        if (at % SPREAD == 0) copy(cur, at / SPREAD, ra2, rb2);
       });
     } else {
       mfmas(a1, b1, nothing);
@@ -348,12 +375,16 @@ TM_DEV void gemm_w4(const TmGemmArgs &p) {
 
 }  // namespace
 
-#define TM_GEMM_W4(NAME, T, EPI)                                                               \
+#define TM_GEMM_W4(NAME, T, EPI, AK, BK)                                                       \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void \
   NAME(TmGemmArgs p) {                                                                         \
-    gemm_w4<T, EPI>(p);                                                                        \
+    gemm_w4<T, EPI, AK, BK>(p);                                                                \
   }
-TM_GEMM_W4(tm_gemm_w4_bf16, bf16_t, EPI_NONE)
-TM_GEMM_W4(tm_gemm_w4_f16, f16_t, EPI_NONE)
-TM_GEMM_W4(tm_sae_w4_bf16, bf16_t, EPI_BIAS_RELU)
-TM_GEMM_W4(tm_sae_w4_f16, f16_t, EPI_BIAS_RELU)
+TM_GEMM_W4(tm_gemm_w4_bf16, bf16_t, EPI_NONE, true, false)
+TM_GEMM_W4(tm_gemm_w4_f16, f16_t, EPI_NONE, true, false)
+TM_GEMM_W4(tm_gemm_w4_nt_bf16, bf16_t, EPI_NONE, true, true)
+TM_GEMM_W4(tm_gemm_w4_nt_f16, f16_t, EPI_NONE, true, true)
+TM_GEMM_W4(tm_gemm_w4_tn_bf16, bf16_t, EPI_NONE, false, false)
+TM_GEMM_W4(tm_gemm_w4_tn_f16, f16_t, EPI_NONE, false, false)
+TM_GEMM_W4(tm_sae_w4_bf16, bf16_t, EPI_BIAS_RELU, true, false)
+TM_GEMM_W4(tm_sae_w4_f16, f16_t, EPI_BIAS_RELU, true, false)

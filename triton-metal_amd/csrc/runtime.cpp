@@ -712,12 +712,14 @@ void choose_gemm(Plan &plan, const TmGemmArgs &p, const BuiltinSpec &spec, const
                           kg == 4 ? "_k4" : kg == 2 ? "_k2" : "", el);
     plan.grid[0] = (unsigned)tiles;
     plan.block = (unsigned)(2 * tile * kg);
-    /* whole row-major 256 x 256 tiles: the 4-wave kernel (gemm_w4.hip), whose
-     * copies address a step's 256 rows of A and 64 rows of B through one
-     * 32-bit buffer range each */
-    if (gemm_w4_enabled() && nn && whole && big && (int64_t)p.sam * 512 <= INT32_MAX &&
-        (int64_t)p.sbk * 128 <= INT32_MAX) {
-      plan.variant = format("tm_%s_w4_%s", family, el);
+    /* whole 256 x 256 tiles: the 4-wave kernel (gemm_w4.hip), whose copies
+     * address a step's tile of each operand through one 32-bit buffer range:
+     * 256 stored rows of a K-contiguous operand (A row-major, B transposed),
+     * 64 of the other kind */
+    const int64_t a_rows = a_n ? (int64_t)p.sam * 512 : (int64_t)p.sak * 128;
+    const int64_t b_rows = b_t ? (int64_t)p.sbn * 512 : (int64_t)p.sbk * 128;
+    if (gemm_w4_enabled() && whole && big && a_rows <= INT32_MAX && b_rows <= INT32_MAX) {
+      plan.variant = format("tm_%s_w4%s_%s", family, nt ? "_nt" : tn ? "_tn" : "", el);
       plan.block = 256;
     }
   } else {
