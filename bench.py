@@ -72,7 +72,17 @@ def parse():
     ap.add_argument("--profile-pass", action="store_true",
                     help="for rocprofv3 --pmc runs: one copy kernel of known size (the "
                          "FETCH_SIZE / WRITE_SIZE calibration) and one dispatch of each hot kernel")
-    return ap.parse_args()
+    ap.add_argument("--operand-data", choices=OPERAND_DATA, default="normal",
+                    help="with --profile-pass: the operands' values (normal: N(0,1) as everywhere "
+                         "else; trunc4: N(0,1) with the low 4 mantissa bits cleared; zeros)")
+    ap.add_argument("--data-study", action="store_true",
+                    help="time the config 5 attention kernels, the 8192^3 GEMM and the SAE encoder "
+                         "on each kind of --operand-data (same shapes and instruction streams) as "
+                         "one JSON line and exit")
+    args = ap.parse_args()
+    if args.operand_data != "normal" and not args.profile_pass:
+        ap.error("--operand-data applies to --profile-pass only; the benchmark uses N(0,1)")
+    return args
 
 
 #: A plain device copy, the calibration kernel for rocprof's HBM byte counters.
@@ -192,10 +202,43 @@ def vendor_reference():
     return out
 
 
+#: Kinds of operand values for the data study: the MFMA-dense kernels run
+#: slower on operands whose bits change more (the chip lowers its clock under
+#: the power drawn), so the same kernel is timed on N(0,1), on N(0,1) with
+#: fewer mantissa bits, and on zeros.
+OPERAND_DATA = ("normal", "trunc4", "zeros")
+_operand_data = "normal"
+
+
 def normal_bf16(shape, seed):
+    """N(0,1) from `seed` as bf16 bits; under the data study, transformed to
+    the current kind of operand data."""
     from triton_metal.buffer import bf16_bits
     rng = np.random.default_rng(seed)
-    return bf16_bits(rng.standard_normal(shape, dtype=np.float32))
+    x = bf16_bits(rng.standard_normal(shape, dtype=np.float32))
+    if _operand_data == "trunc4":
+        x &= np.uint16(0xFFF0)
+    elif _operand_data == "zeros":
+        x[...] = 0
+    return x
+
+
+def data_study(core, ops, sample_ms):
+    """Kernel times on each kind of operand data, one process, same shapes."""
+    global _operand_data
+    out = {}
+    try:
+        for kind in OPERAND_DATA:
+            _operand_data = kind
+            _, per = bench_attention(core, ops, 4, 32, 4096, 128, True, 3, 3, sample_ms)
+            rec = {name: round(v["ms"], 4) for name, v in per.items()}
+            rec["gemm_bf16_8192"] = round(bench_gemm(core, ops, 8192, 3, sample_ms)[0], 4)
+            rec["sae_encode_bf16_8192x2048x16384"] = round(
+                bench_sae(core, ops, 8192, 2048, 16384, 3, sample_ms)[0], 4)
+            out[kind] = rec
+    finally:
+        _operand_data = "normal"
+    return out
 
 
 def kernel_ms(core, kernel, grid, kinds, values, sample_ms):
@@ -631,7 +674,13 @@ def main():
         print(json.dumps({"probes": bench_probes.run(), "device": core.device_name()}))
         return
     if args.profile_pass:
+        global _operand_data
+        _operand_data = args.operand_data
         profile_pass(core, ops)
+        return
+    if args.data_study:
+        print(json.dumps({"data_study_ms": data_study(core, ops, args.sample_ms),
+                          "device": core.device_name()}))
         return
 
     components = {}

@@ -50,3 +50,20 @@ def test_verifier_records_and_fails():
     assert v.failures == ["case.dk: error 3.000e-02 > 0.02"]
     v.add("other", "o", float("inf"), 2e-2)
     assert len(v.failures) == 2
+
+
+def test_operand_data_kinds():
+    """The data study's operands: N(0,1) bf16 bits by default (the benchmark's
+    data), the same values with the low 4 mantissa bits cleared, or zeros;
+    the default is restored after a study."""
+    base = bench.normal_bf16((64, 32), 5)
+    assert base.dtype == np.uint16 and np.count_nonzero(base & 0xF) > 0
+    try:
+        bench._operand_data = "trunc4"
+        t = bench.normal_bf16((64, 32), 5)
+        assert np.array_equal(t, base & np.uint16(0xFFF0))
+        bench._operand_data = "zeros"
+        assert not np.any(bench.normal_bf16((64, 32), 5))
+    finally:
+        bench._operand_data = "normal"
+    assert np.array_equal(bench.normal_bf16((64, 32), 5), base)
