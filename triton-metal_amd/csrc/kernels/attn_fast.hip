@@ -303,12 +303,13 @@ template <> struct PBias<f16_t> { static constexpr float B = 2.f; };
 template <typename T, int D, bool CAUSAL>
 TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   constexpr int QT = 2, BM = 128, QW = 32, BN = 64; /* query tiles per wave, queries per workgroup / wave, keys per block */
+  constexpr int KT = BN / 16, KK = BN / 32;         /* 16-key tiles of S^T, 32-key halves of P V */
   constexpr int KS = D / 32;            /* k-steps of the S^T contraction */
   constexpr int DT = D / 16;            /* 16-wide d tiles of O^T */
   constexpr int TILE = BN * D * 2;
-  constexpr int NM1 = 4 * KS * QT;      /* S MFMAs per block */
-  constexpr int NM2 = (DT + 1) * 2 * QT; /* P V MFMAs per block, row sums included */
-  constexpr int VS = QT * 32;           /* softmax slots per iteration (4 per element pair) */
+  constexpr int NM1 = KT * KS * QT;     /* S MFMAs per block */
+  constexpr int NM2 = (DT + 1) * KK * QT; /* P V MFMAs per block, row sums included */
+  constexpr int VS = QT * BN / 2;       /* softmax slots per iteration (4 per element pair) */
   constexpr int LA = 2;                 /* operands read ahead */
   constexpr float BIAS = PBias<T>::B;
   __shared__ __align__(1024) char lds[4 * TILE];
@@ -379,17 +380,19 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   /* scores of the block whose softmax runs next and the packed P^T B operands
    * [qt][kk] of the block whose P V runs next, each in two sets that the
    * iterations of the interior loop alternate */
-  f32x4 s[4][QT], s2[4][QT];
-  u32x4 pf[QT][2], pf2[QT][2];
+  f32x4 s[KT][QT], s2[KT][QT];
+  u32x4 pf[QT][KK], pf2[QT][KK];
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) pf[qt][0] = pf[qt][1] = (u32x4){0u, 0u, 0u, 0u};
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) pf[qt][kk] = (u32x4){0u, 0u, 0u, 0u};
 
-  auto mask_block = [&](f32x4 (&sc)[4][QT], int k0) {
+  auto mask_block = [&](f32x4 (&sc)[KT][QT], int k0) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       const int qi = qw0 + qt * 16 + c;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int key = k0 + kt * 16 + 4 * g + r;
@@ -398,20 +401,20 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
     }
   };
   /* exact row maxima of a block times qk_scale, reduced over the 4 lane groups */
-  auto row_max = [&](const f32x4 (&sc)[4][QT], float (&out)[QT]) {
+  auto row_max = [&](const f32x4 (&sc)[KT][QT], float (&out)[QT]) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       float mx = vmax(sc[0][qt][0], sc[0][qt][1]);
 #pragma unroll
-      for (int e = 2; e < 16; e += 2)
+      for (int e = 2; e < 4 * KT; e += 2)
         mx = vmax(vmax(mx, sc[e >> 2][qt][e & 3]), sc[e >> 2][qt][(e & 3) + 1]);
       out[qt] = group4_max(mx) * qk_scale;
     }
   };
   /* S^T of one block from K fragments read by `kfrag(kt, ks)` */
-  auto scores = [&](f32x4 (&sc)[4][QT], auto kfrag) {
+  auto scores = [&](f32x4 (&sc)[KT][QT], auto kfrag) {
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
+    for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) sc[kt][qt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -445,8 +448,8 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
    * vrd/krd: LDS addresses of the V(j-1) and K(j+1) tiles; vdst/kdst: where
    * V(j) and K(j+2) are copied. */
   auto iteration = [&](auto pv_tag, auto sm_tag, auto sn_tag, auto edge_tag, uint32_t vrd,
-                       uint32_t krd, uint32_t vdst, uint32_t kdst, int j, f32x4 (&s)[4][QT],
-                       f32x4 (&sn)[4][QT], u32x4 (&pf)[QT][2], u32x4 (&pn)[QT][2]) {
+                       uint32_t krd, uint32_t vdst, uint32_t kdst, int j, f32x4 (&s)[KT][QT],
+                       f32x4 (&sn)[KT][QT], u32x4 (&pf)[QT][KK], u32x4 (&pn)[QT][KK]) {
     constexpr bool PV = decltype(pv_tag)::value;
     constexpr bool SM = decltype(sm_tag)::value;
     constexpr bool SN = decltype(sn_tag)::value;
@@ -478,7 +481,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
         if constexpr (dt == DT) opnd[o] = ones;
         else opnd[o] = lds_read_kmajor(vrd + voff[dt], 32 * kk * D * 2, (32 * kk + 16) * D * 2);
       } else if constexpr (o < NM / QT) {
-        constexpr int b = o - NA / QT, kt = b % 4, ks = b / 4;
+        constexpr int b = o - NA / QT, kt = b % KT, ks = b / KT;
         opnd[o] = lds_read16(krd + koff[ks] + kt * 16 * D * 2);
       }
     };
@@ -489,7 +492,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
     uint32_t wd = 0, wprev = 0;
     auto vslot = [&](auto vv) {
       constexpr int v = decltype(vv)::value;
-      constexpr int u = v / 4, beat = v % 4, qt = u / 8, kk = (u / 4) % 2, w = u % 4;
+      constexpr int u = v / 4, beat = v % 4, qt = u / (BN / 8), kk = (u / 4) % KK, w = u % 4;
       constexpr int e0 = 2 * w, e1 = 2 * w + 1;
       if constexpr (beat == 0) {
         px[0] = __builtin_fmaf(s[2 * kk + (e0 >> 2)][qt][e0 & 3], qk_scale, -mb[qt]);
@@ -518,7 +521,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
     }
     if constexpr (SN) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) sn[kt][qt] = (f32x4){0.f, 0.f, 0.f, 0.f};
     }
@@ -535,7 +538,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
         constexpr int kk = o / (DT + 1), dt = (o % (DT + 1) + DT) % (DT + 1);
         acc[dt][qt] = mfma_16x16x32(as_vec8<T>(opnd[o]), as_vec8<T>(pf[qt][kk]), acc[dt][qt]);
       } else {
-        constexpr int b = o - NA / QT, kt = b % 4, ks = b / 4;
+        constexpr int b = o - NA / QT, kt = b % KT, ks = b / KT;
         sn[kt][qt] = mfma_16x16x32(as_vec8<T>(opnd[o]), as_vec8<T>(qf[qt][ks]), sn[kt][qt]);
       }
       if constexpr (SM)
@@ -549,7 +552,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
        * redo P, and scale O and the row sums, which hold the P V of every
        * block computed under the old offsets (all issued above) */
       if (__builtin_amdgcn_ballot_w64((big & 0x40004000u) != 0) != 0) {
-        f32x4 sr[4][QT];
+        f32x4 sr[KT][QT];
         scores(sr, [&](int kt, int ks) {
           const int key = min(k0 + kt * 16 + c, n - 1);
           return *(const u32x4 *)(Kg + (int64_t)key * ss + ks * 32 + 8 * g);
@@ -563,7 +566,7 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
           const float alpha = fast_exp2(mb[qt] - m_new);
           mb[qt] = m_new;
 #pragma unroll
-          for (int kk = 0; kk < 2; ++kk)
+          for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
               const int e0 = 2 * w, e1 = 2 * w + 1;
@@ -583,13 +586,13 @@ TM_DEV void attn_fwd_fast(const TmAttnFwdArgs &p) {
   using F_ = std::integral_constant<bool, false>;
   auto take_second_set = [&]() {
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+    for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) s[kt][qt] = s2[kt][qt];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      pf[qt][0] = pf2[qt][0];
-      pf[qt][1] = pf2[qt][1];
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) pf[qt][kk] = pf2[qt][kk];
     }
   };
 
