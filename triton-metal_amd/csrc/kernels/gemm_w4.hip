@@ -191,10 +191,13 @@ TM_DEV void gemm_w4(const TmGemmArgs &p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  /* tile order: each XCD a contiguous range, walked 8 tile rows at a time */
+  /* tile order: each XCD a contiguous range, walked 4 tile rows at a time
+   * (measured against 2, 8 and 16 on one box, alternating runs, TFLOP/s:
+   * 8192^3 1309 / 1271-1275 / 1299 / 1275-1277, SAE 1171-1172 / 1176-1177 /
+   * 1150-1152 / 1127-1128, 4096^3 1254-1255 / 1251-1253 / 1241-1243 / 1248) */
   const int mt = p.m / W4_TILE, nt = p.n / W4_TILE;
   const int logical = w4_xcd_remap(blockIdx.x, gridDim.x);
-  constexpr int GROUP = 8;
+  constexpr int GROUP = 4;
   const int per_group = GROUP * nt;
   const int group = logical / per_group;
   const int first_m = group * GROUP;
