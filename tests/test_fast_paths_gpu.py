@@ -562,3 +562,49 @@ def test_four_wave_gemm_transposed(element, layout, m, n, k, lda, ldb, ldc, devi
     assert np.all(np.isfinite(c[:m, :n]))
     assert T.hybrid_error(c[:m, :n], want) <= 2e-2
     assert np.all(c[:m, n:] == -7.0) and np.all(c[m:] == -7.0)
+
+
+@pytest.mark.parametrize("operand,stride,expect", [
+    ("b", 16777208, "w4"),    # B row-major: 64 rows at this stride span just under 2^31 bytes
+    ("b", 16777216, "fast"),  # one 8-element step further: past the 32-bit range
+    ("a", 4194296, "w4"),     # A row-major: 256 rows at this stride span just under 2^31 bytes
+    ("a", 4194304, "fast"),
+])
+def test_four_wave_gemm_buffer_range_limit(operand, stride, expect, device):
+    """The 4-wave kernel addresses a step's tile of each operand through one
+    buffer resource with 32-bit offsets: 256 stored rows of a K-contiguous
+    operand (A row-major), 64 of the other kind (B row-major).  At the largest
+    row stride whose offsets and range stay below 2^31 bytes the planner takes
+    it, and every element is right; one step further it takes the 8-wave
+    kernel, whose copies use 64-bit addresses.  Only the rows the GEMM reads
+    are written (the A buffers span about 34 GB, the B buffers 2 GB)."""
+    from triton_metal.buffer import bf16_bits
+    m = n = 4096
+    k = 64
+    rng = np.random.default_rng(stride)
+    a = round_to(rng.standard_normal((m, k), dtype=np.float32), "bf16")
+    b = round_to(rng.standard_normal((k, n), dtype=np.float32), "bf16")
+    lda, ldb = (stride, n) if operand == "a" else (k, stride)
+    rows, ld, dense = (m, lda, a) if operand == "a" else (k, ldb, b)
+    strided = _core.alloc_buffer(((rows - 1) * ld + dense.shape[1]) * 2)
+    other = DeviceBuffer.from_numpy(b if operand == "a" else a, "bfloat16")
+    c = DeviceBuffer((m, n), "bfloat16")
+    try:
+        bits = bf16_bits(dense)
+        for i in range(rows):
+            row = np.ascontiguousarray(bits[i])
+            _core.buffer_write(strided, i * ld * 2, row.ctypes.data, row.nbytes)
+        ha, hb = (strided, other.tm_handle) if operand == "a" else (other.tm_handle, strided)
+        kern = ops.library("bf16").kernels["matmul_kernel"]
+        kinds = [_core.ARG_BUFFER] * 3 + [_core.ARG_I32] * 9
+        _core.launch(kern, (m // 64, n // 64, 1), 128, kinds,
+                     [ha, hb, c.tm_handle, m, n, k, lda, 1, ldb, 1, n, 1])
+        variant = _core.kernel_variant(kern)
+        got = c.float32()
+    finally:
+        _core.free_buffer(strided)
+        other.free()
+        c.free()
+    assert variant == f"tm_gemm_{expect}_bf16"
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    assert T.hybrid_error(got, want) <= 2e-2
